@@ -1,0 +1,93 @@
+/* metile_amd — C ABI of the MI355X (gfx950) quantized-projection kernels.
+ *
+ * Every entry point takes caller-owned DEVICE pointers, plain integer sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL is the default stream), enqueues its kernels on that
+ * stream and returns without synchronising. The library allocates nothing: split-K partial
+ * sums and the MLP hidden activation live in a caller-provided workspace whose size the
+ * matching *_workspace_bytes function reports. The first 64 KiB of every workspace hold
+ * split-K arrival counters at fixed places; a workspace must be zero-filled once before
+ * its first use; every call leaves its counter region zeroed again. Calls that share one
+ * workspace must be ordered (same stream); calls on different streams need different
+ * workspaces.
+ *
+ * Return value: MT_OK (0) or a negative mt_status. The message of the last failure on the
+ * calling thread is available from mt_last_error(). Nothing throws across this boundary.
+ *
+ * Tensor formats (row-major, contiguous):
+ *   x, residual, y, h     16-bit floats [M, K] / [M, N] (dtype MT_BF16 or MT_F16, as uint16)
+ *   w_q                   uint32 [N, K*bits/32], MLX affine packing: code k of a row sits in
+ *                         word k/(32/bits) at bit (k % (32/bits))*bits (low bits first)
+ *   scales, biases        16-bit floats [N, K/group_size], same dtype as x
+ *   dense weights         16-bit floats [N, K]
+ */
+#ifndef METILE_AMD_H
+#define METILE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mt_status {
+  MT_OK = 0,
+  MT_ERR_INVALID_ARGUMENT = -1, /* null pointer, bad shape, unsupported bits/group/dtype */
+  MT_ERR_WORKSPACE = -2,        /* workspace missing or smaller than required */
+  MT_ERR_HIP = -3               /* a HIP runtime call failed (launch error) */
+} mt_status;
+
+typedef enum mt_dtype { MT_BF16 = 0, MT_F16 = 1 } mt_dtype;
+
+/* Library version string. */
+const char* mt_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mt_last_error(void);
+
+/* Workspace bytes mt_affine_qmv (nproj = 1) or mt_affine_swiglu (nproj = 2) needs. */
+size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj);
+
+/* y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/G] + b[n, k/G]) (+ residual[m, n]).
+ * Replaces mlx_affine_qmv (metile/backends/mlx_quantized.py:691-714) and, with a residual,
+ * mlx_affine_residual_qmv (metile/backends/mlx_quantized.py:1538-1624); the kernels they
+ * bind are kernels/affine_qmv.py:57-132. bits in {4, 8}; group_size a multiple of 64 that
+ * divides K; K % 64 == 0; N % 32 == 0; any M >= 1 (rows beyond 32 run in 32-row chunks). */
+int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
+                  const void* residual, void* y, int M, int K, int N, int group_size, int bits,
+                  int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* h[m, n] = silu(x @ Wg^T)[m, n] * (x @ Wu^T)[m, n], gate and up accumulated in fp32 from one
+ * activation load and combined before the single output rounding. Replaces mlx_affine_swiglu
+ * / mlx_affine_swiglu_qmv (metile/backends/mlx_quantized.py:717-751,1645-1720) and the kernel
+ * kernels/affine_qmv.py:135-214. Shape rules as mt_affine_qmv. */
+int mt_affine_swiglu(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                     const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                     const void* up_biases, void* h, int M, int K, int N, int group_size,
+                     int bits, int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for mt_affine_mlp (hidden activation plus split-K partials). */
+size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bits);
+
+/* y = down(swiglu(x)) (+ residual), x [M, H], gate/up [I, H], down [H, I]. The hidden
+ * activation is rounded to the activation dtype between the two kernels, as the reference
+ * executor's two dispatches do. Replaces the execute() closure of mlx_affine_mlp_executor
+ * (metile/backends/mlx_quantized.py:1770-1832). */
+int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                  const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                  const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                  const void* down_biases, const void* residual, void* y, int M, int H, int I,
+                  int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* out[n, k] = q[n, k] * s[n, k/G] + b[n, k/G] in fp32 (bit-exact dequantization, the decode
+ * step of kernels/affine_qmv.py:41-51). Any group_size dividing K with K % (32/bits) == 0. */
+int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,
+                         float* out, int N, int K, int group_size, int bits, int dtype,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* METILE_AMD_H */

@@ -1,0 +1,35 @@
+"""metile_amd — MI355X (gfx950) kernels for meTile's quantized-projection hot path.
+
+Affine 4/8-bit quantized QMV, fused SwiGLU and the quantized MLP, written as hand-written HIP
+kernels behind a C ABI (``include/metile_amd.h``) and exposed here on torch tensors with the
+reference's call surface (``metile/backends/mlx_quantized.py``).
+"""
+
+from ._lib import MetileError, version
+from .quantized import (
+    affine_dequantize,
+    affine_mlp,
+    affine_qmv,
+    affine_swiglu,
+    mlx_affine_mlp_executor,
+    mlx_affine_qmv,
+    mlx_affine_residual_qmv,
+    mlx_affine_swiglu,
+    mlx_affine_swiglu_executor,
+    mlx_affine_swiglu_qmv,
+)
+
+__all__ = [
+    "MetileError",
+    "affine_dequantize",
+    "affine_mlp",
+    "affine_qmv",
+    "affine_swiglu",
+    "mlx_affine_mlp_executor",
+    "mlx_affine_qmv",
+    "mlx_affine_residual_qmv",
+    "mlx_affine_swiglu",
+    "mlx_affine_swiglu_executor",
+    "mlx_affine_swiglu_qmv",
+    "version",
+]

@@ -1,0 +1,227 @@
+// extern "C" boundary of libmetile_amd.so: argument validation, workspace layout, split-K
+// planning and error reporting. No allocation, no synchronisation, no exceptions across the ABI.
+#include "../../include/metile_amd.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <string>
+
+#include "affine_qmv.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(MT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+constexpr int kRowChunk = 32;  // rows per small-row dispatch
+
+// Every workspace starts with a fixed region of split-K arrival counters (one per 32-column
+// strip), shared by all shapes so that each counter is always found at the same place; every
+// call leaves the counters it used at zero. Partial sums follow the counter region.
+constexpr size_t kCounterBytes = 64 * 1024;
+constexpr int kMaxStrips = (int)(kCounterBytes / 4);
+
+// Split-K plan of the small-row kernel for one (K, N): enough workgroups to cover the chip
+// about twice, at least four K steps per split, and no split longer than kMaxStepsPerSplit.
+// Depends only on K and N, never on the row count.
+struct Plan {
+  int ksplit;
+  int steps_per_split;
+};
+
+Plan plan_qmv(int K, int N) {
+  const int steps = K / 64;
+  const int strips = N / 32;
+  int ksplit = (512 + strips - 1) / strips;
+  const int max_split = steps / 4 > 0 ? steps / 4 : 1;
+  if (ksplit > max_split) ksplit = max_split;
+  const int min_split = (steps + mt::kMaxStepsPerSplit - 1) / mt::kMaxStepsPerSplit;
+  if (ksplit < min_split) ksplit = min_split;
+  if (const char* env = std::getenv("METILE_AMD_KSPLIT")) {
+    const int forced = std::atoi(env);
+    if (forced >= min_split && forced <= steps) ksplit = forced;
+  }
+  if (ksplit < 1) ksplit = 1;
+  Plan p;
+  p.steps_per_split = (steps + ksplit - 1) / ksplit;
+  p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
+  return p;
+}
+
+size_t qmv_workspace(int M, int K, int N, int nproj) {
+  const Plan plan = plan_qmv(K, N);
+  if (plan.ksplit <= 1) return 0;
+  const int rows = M < kRowChunk ? M : kRowChunk;
+  return kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+}
+
+int check_affine(const char* op, int M, int K, int N, int group_size, int bits, int dtype) {
+  if (bits != 4 && bits != 8)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": bits must be 4 or 8");
+  if (dtype != MT_BF16 && dtype != MT_F16)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": dtype must be MT_BF16 or MT_F16");
+  if (M < 1 || K < 1 || N < 1)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": M, K and N must be positive");
+  if (group_size < 64 || group_size % 64 || K % group_size)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": group_size must be a multiple of 64 that divides K");
+  if (K % 64 || N % 32)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": K must be a multiple of 64 and N a multiple of 32");
+  if (N / 32 > kMaxStrips)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": N larger than " +
+                                             std::to_string(kMaxStrips * 32) + " is unsupported");
+  const size_t wbytes = (size_t)N * K * bits / 8;
+  const size_t xbytes = (size_t)(M < kRowChunk ? M : kRowChunk) * K * 2;
+  if (wbytes >= (1ull << 31) || xbytes >= (1ull << 31) || (size_t)M * N >= (1ull << 31))
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": tensor larger than 2 GiB");
+  return MT_OK;
+}
+
+int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2],
+            const void* const s[2], const void* const b[2], const void* residual, void* y,
+            int M, int K, int N, int group_size, int bits, int dtype, void* workspace,
+            size_t workspace_bytes, void* stream) {
+  int st = check_affine(op, M, K, N, group_size, bits, dtype);
+  if (st) return st;
+  if (!x || !y) return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null x or output");
+  for (int q = 0; q < nproj; ++q)
+    if (!w[q] || !s[q] || !b[q])
+      return fail(MT_ERR_INVALID_ARGUMENT,
+                  std::string(op) + ": null packed weight, scales or biases");
+  const size_t need = qmv_workspace(M, K, N, nproj);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
+                                      " bytes required, got " + std::to_string(workspace_bytes));
+  const Plan plan = plan_qmv(K, N);
+  const hipStream_t hs = static_cast<hipStream_t>(stream);
+  for (int r0 = 0; r0 < M; r0 += kRowChunk) {
+    const int rows = (M - r0) < kRowChunk ? (M - r0) : kRowChunk;
+    mt::QmvParams p{};
+    p.x = static_cast<const uint16_t*>(x) + (size_t)r0 * K;
+    for (int q = 0; q < nproj; ++q) {
+      p.w[q] = w[q];
+      p.s[q] = static_cast<const uint16_t*>(s[q]);
+      p.b[q] = static_cast<const uint16_t*>(b[q]);
+    }
+    p.residual = residual ? static_cast<const uint16_t*>(residual) + (size_t)r0 * N : nullptr;
+    p.y = static_cast<uint16_t*>(y) + (size_t)r0 * N;
+    if (plan.ksplit > 1) {
+      p.counters = static_cast<uint32_t*>(workspace);
+      p.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    }
+    p.M = rows;
+    p.K = K;
+    p.N = N;
+    p.G = group_size;
+    p.ksplit = plan.ksplit;
+    p.steps_per_split = plan.steps_per_split;
+    const hipError_t e = mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
+    if (e != hipSuccess) return hip_fail(e, op);
+  }
+  return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mt_version(void) { return "metile_amd 0.1.0 (gfx950)"; }
+
+const char* mt_last_error(void) { return g_last_error.c_str(); }
+
+size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj) {
+  if (check_affine("mt_affine_qmv_workspace_bytes", M, K, N, group_size, bits, MT_BF16))
+    return 0;
+  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1);
+}
+
+int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
+                  const void* residual, void* y, int M, int K, int N, int group_size, int bits,
+                  int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const uint32_t* w[2] = {w_q, nullptr};
+  const void* s[2] = {scales, nullptr};
+  const void* b[2] = {biases, nullptr};
+  return run_qmv("mt_affine_qmv", 1, x, w, s, b, residual, y, M, K, N, group_size, bits, dtype,
+                 workspace, workspace_bytes, stream);
+}
+
+int mt_affine_swiglu(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                     const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                     const void* up_biases, void* h, int M, int K, int N, int group_size,
+                     int bits, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const uint32_t* w[2] = {gate_w, up_w};
+  const void* s[2] = {gate_scales, up_scales};
+  const void* b[2] = {gate_biases, up_biases};
+  return run_qmv("mt_affine_swiglu", 2, x, w, s, b, nullptr, h, M, K, N, group_size, bits,
+                 dtype, workspace, workspace_bytes, stream);
+}
+
+size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bits) {
+  if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
+      check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
+    return 0;
+  const size_t a = qmv_workspace(M, H, I, 2);
+  const size_t b = qmv_workspace(M, I, H, 1);
+  const size_t split = align_up(a > b ? a : b);
+  return (split > kCounterBytes ? split : kCounterBytes) + align_up((size_t)M * I * 2);
+}
+
+int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                  const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                  const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                  const void* down_biases, const void* residual, void* y, int M, int H, int I,
+                  int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  int st = check_affine("mt_affine_mlp", M, H, I, group_size, bits, dtype);
+  if (st) return st;
+  st = check_affine("mt_affine_mlp", M, I, H, group_size, bits, dtype);
+  if (st) return st;
+  const size_t need = mt_affine_mlp_workspace_bytes(M, H, I, group_size, bits);
+  if (!workspace || workspace_bytes < need)
+    return fail(MT_ERR_WORKSPACE, "mt_affine_mlp: workspace of " + std::to_string(need) +
+                                      " bytes required, got " + std::to_string(workspace_bytes));
+  // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
+  const size_t hidden_off = need - align_up((size_t)M * I * 2);
+  void* h = static_cast<char*>(workspace) + hidden_off;
+  st = mt_affine_swiglu(x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h, M, H,
+                        I, group_size, bits, dtype, workspace, hidden_off, stream);
+  if (st) return st;
+  return mt_affine_qmv(h, down_w, down_scales, down_biases, residual, y, M, I, H, group_size,
+                       bits, dtype, workspace, hidden_off, stream);
+}
+
+int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,
+                         float* out, int N, int K, int group_size, int bits, int dtype,
+                         void* stream) {
+  if (bits != 4 && bits != 8)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_dequantize: bits must be 4 or 8");
+  if (dtype != MT_BF16 && dtype != MT_F16)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_dequantize: dtype must be MT_BF16 or MT_F16");
+  if (N < 1 || K < 1 || group_size < 1 || K % group_size || K % (32 / bits) ||
+      group_size % (32 / bits))
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "mt_affine_dequantize: group_size must divide K and hold whole packed words");
+  if (!w_q || !scales || !biases || !out)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_dequantize: null pointer");
+  const hipError_t e = mt::launch_affine_dequantize(
+      w_q, static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases), out, N, K,
+      group_size, bits, dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_affine_dequantize");
+  return MT_OK;
+}
+
+}  // extern "C"

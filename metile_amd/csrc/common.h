@@ -1,0 +1,168 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of metile_amd.
+//
+// Conventions used by every kernel in this directory:
+//  * activations, scales, biases and outputs are 16-bit floats (bf16 or f16) carried as
+//    uint16_t bit patterns; accumulation is fp32;
+//  * packed affine weights are MLX's output-major uint32 words, code k of a row at word
+//    k / (32/bits), shift (k % (32/bits)) * bits (low bits first along K);
+//  * all global reads go through raw buffer loads, whose hardware range check returns zero
+//    for any offset at or beyond the buffer size; kOOB is used to switch a lane's load off.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mt {
+
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+enum Dtype : int { kBF16 = 0, kF16 = 1 };
+
+// Offsets at or above every buffer size used here read as zero.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  // Word 3 = 0x00020000: raw (unswizzled, untyped) dword access on gfx9-family parts.
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+__device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ u32x2 load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint16_t load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+// ---- 16-bit float conversions ----------------------------------------------------------
+
+template <int DT>
+__device__ __forceinline__ float act_to_f32(uint32_t bits16) {
+  if constexpr (DT == kBF16) {
+    return __uint_as_float(bits16 << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+  }
+}
+
+// Round-to-nearest-even conversion of fp32 to the activation type.
+template <int DT>
+__device__ __forceinline__ uint16_t f32_to_act(float f) {
+  if constexpr (DT == kBF16) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+  } else {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+}
+
+// ---- MFMA 32x32x16 (fp32 accumulate) -----------------------------------------------------
+// Lane l supplies A[i = l%32][k = 8*(l/32) + 0..7] and B[k = 8*(l/32) + 0..7][j = l%32];
+// the result element (i, j) lives in lane j + 32*((i/4)%2), register 4*(i/8) + i%4.
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == kBF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Row of the 32x32 output tile held in register r of a lane in half h (= lane / 32).
+__device__ __forceinline__ constexpr int mfma32_row(int r, int h) {
+  return 8 * (r / 4) + 4 * h + (r % 4);
+}
+
+// ---- code -> 16-bit float unpack (exact) -------------------------------------------------
+// A 4-bit code q is written into the low mantissa bits of a 16-bit float whose exponent makes
+// the mantissa step exactly 1: bf16 0x4300|q == 128 + q, f16 0x6400|q == 1024 + q. 8-bit
+// codes use f16 0x6400|q == 1024 + q, or for bf16 an exact int -> fp32 -> bf16 conversion
+// (integers below 256 have at most 8 significant bits). kCodeOffset is the constant added.
+
+template <int BITS, int DT>
+struct CodeOffset {
+  static constexpr float value = (DT == kF16) ? 1024.0f : (BITS == 4 ? 128.0f : 0.0f);
+};
+
+// 8 nibbles of one word -> 8 values in K order, packed two per uint32.
+template <int DT>
+__device__ __forceinline__ u32x4 unpack_u4(uint32_t w) {
+  constexpr uint32_t kMagic = (DT == kBF16) ? 0x43434343u : 0x64646464u;
+  const uint32_t a = w & 0x0F0F0F0Fu;          // codes 0, 2, 4, 6 (one per byte)
+  const uint32_t b = (w >> 4) & 0x0F0F0F0Fu;   // codes 1, 3, 5, 7
+  const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // codes 0 1 2 3
+  const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // codes 4 5 6 7
+  u32x4 out;
+  out.x = __builtin_amdgcn_perm(kMagic, lo, 0x04010400u);
+  out.y = __builtin_amdgcn_perm(kMagic, lo, 0x04030402u);
+  out.z = __builtin_amdgcn_perm(kMagic, hi, 0x04010400u);
+  out.w = __builtin_amdgcn_perm(kMagic, hi, 0x04030402u);
+  return out;
+}
+
+// 4 bytes of one word -> 4 values in K order, packed two per uint32.
+template <int DT>
+__device__ __forceinline__ u32x2 unpack_u8(uint32_t w) {
+  u32x2 out;
+  if constexpr (DT == kF16) {
+    out.x = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+    out.y = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+  } else {
+    const uint32_t f0 = __float_as_uint((float)(w & 0xFFu));
+    const uint32_t f1 = __float_as_uint((float)((w >> 8) & 0xFFu));
+    const uint32_t f2 = __float_as_uint((float)((w >> 16) & 0xFFu));
+    const uint32_t f3 = __float_as_uint((float)(w >> 24));
+    out.x = __builtin_amdgcn_perm(f1, f0, 0x07060302u);
+    out.y = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
+  }
+  return out;
+}
+
+// The two 16-bit floats of a packed pair, widened to fp32 (element 0 is the low half).
+template <int DT>
+__device__ __forceinline__ float lo16(uint32_t w) {
+  if constexpr (DT == kBF16) return __uint_as_float(w << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xFFFFu));
+}
+template <int DT>
+__device__ __forceinline__ float hi16(uint32_t w) {
+  if constexpr (DT == kBF16) return __uint_as_float(w & 0xFFFF0000u);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// Sum of the 8 16-bit floats held in a u32x4, added to acc in element order in fp32.
+// (Plain adds: a probe of v_dot2_f32_bf16 against ones returned wrong sums for negative
+// inputs, so the dot instructions are not used for this.)
+template <int DT>
+__device__ __forceinline__ float sum8(u32x4 v, float acc) {
+  acc += lo16<DT>(v.x);
+  acc += hi16<DT>(v.x);
+  acc += lo16<DT>(v.y);
+  acc += hi16<DT>(v.y);
+  acc += lo16<DT>(v.z);
+  acc += hi16<DT>(v.z);
+  acc += lo16<DT>(v.w);
+  acc += hi16<DT>(v.w);
+  return acc;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+}  // namespace mt

@@ -1,0 +1,345 @@
+"""Affine quantized projections on torch tensors, backed by the gfx950 HIP kernels.
+
+The public functions keep meTile's MLX-backend call surface
+(``metile/backends/mlx_quantized.py``): the same names, positional/keyword arguments,
+argument meaning and ``ValueError`` guards, but they take and return torch tensors on a ROCm
+device and always run the hand-written HIP kernels through the C ABI (there is no other code
+path to select, so the reference's autotune/fallback arguments are accepted and have no
+effect on the result).
+
+Tensor formats (MLX affine): ``weight`` uint32 (or int32 holding the same bits)
+``[N, K*bits/32]``; ``scales``/``biases`` ``[N, K/group_size]`` in the activation dtype
+(bfloat16 or float16); activations ``[..., K]``.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.MT_BF16, torch.float16: _lib.MT_F16}
+
+# ---------------------------------------------------------------------------------------------
+# workspace cache: one zero-initialised buffer per (device, stream), grown on demand
+# ---------------------------------------------------------------------------------------------
+
+_ws_lock = threading.RLock()
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Return a zero-initialised uint8 workspace of at least ``nbytes`` for the current stream.
+
+    Calls on one stream are ordered, so they may share it; the kernels leave its counter
+    region zeroed after each call.
+    """
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           _stream_handle(device))
+    with _ws_lock:
+        buf = _workspaces.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _workspaces[key] = buf
+        return buf
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("metile_amd operators take ROCm device tensors")
+
+
+def _as_u32(weight: torch.Tensor) -> torch.Tensor:
+    if weight.dtype not in (torch.uint32, torch.int32):
+        raise ValueError("packed affine weights must be uint32 (or int32 holding the same bits)")
+    return weight.contiguous()
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise ValueError("activations must be bfloat16 or float16") from None
+
+
+def _check_params(values, weight, scales, biases, group_size, bits, what):
+    k = values.shape[-1]
+    n = weight.shape[0]
+    if (weight.ndim != 2 or weight.shape[1] * 32 // bits != k
+            or tuple(scales.shape) != (n, k // group_size)
+            or tuple(biases.shape) != (n, k // group_size)):
+        raise ValueError(f"{what} received incompatible quantization parameters")
+    if scales.dtype != values.dtype or biases.dtype != values.dtype:
+        raise ValueError(f"{what} parameters must match the input dtype")
+
+
+# ---------------------------------------------------------------------------------------------
+# general entry points
+# ---------------------------------------------------------------------------------------------
+
+
+def affine_qmv(values, weight, scales, biases, *, group_size=64, bits=4, residual=None):
+    """``values @ dequantize(weight).T (+ residual)`` with fp32 accumulation.
+
+    Semantics of ``mx.quantized_matmul(values, weight, scales, biases, transpose=True)`` as
+    restated by ``kernels/affine_qmv.py:4-132``. Any leading shape; bits 4 or 8; group_size a
+    multiple of 64 dividing K.
+    """
+    if biases is None:
+        raise ValueError("affine QMV requires affine quantization biases")
+    _require_device(values, weight, scales, biases, residual)
+    code = _dtype_code(values.dtype)
+    _check_params(values, weight, scales, biases, group_size, bits, "affine QMV")
+    k = values.shape[-1]
+    n = weight.shape[0]
+    lead = tuple(values.shape[:-1])
+    x = values.reshape(-1, k).contiguous()
+    m = x.shape[0]
+    out = torch.empty(*lead, n, dtype=values.dtype, device=values.device)
+    if m == 0:
+        return out
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (*lead, n) or residual.dtype != values.dtype:
+            raise ValueError("residual must match the affine QMV output shape and dtype")
+        res = residual.reshape(m, n).contiguous()
+    w = _as_u32(weight)
+    s = scales.contiguous()
+    b = biases.contiguous()
+    L = _lib.lib()
+    need = L.mt_affine_qmv_workspace_bytes(m, k, n, group_size, bits, 1)
+    ws = workspace(values.device, need) if need else None
+    _lib.check(L.mt_affine_qmv(
+        x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), _ptr(res), out.data_ptr(),
+        m, k, n, group_size, bits, code, _ptr(ws), 0 if ws is None else ws.numel(),
+        _stream_handle(values.device)))
+    return out
+
+
+def affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                  up_biases, *, group_size=64, bits=4):
+    """Fused ``silu(values @ Wg^T) * (values @ Wu^T)``; gate and up stay in fp32 registers and
+    are combined before the single output rounding (``kernels/affine_qmv.py:135-214``)."""
+    if gate_biases is None or up_biases is None:
+        raise ValueError("affine SwiGLU requires affine quantization biases")
+    _require_device(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                    up_biases)
+    code = _dtype_code(values.dtype)
+    if (gate_weight.shape != up_weight.shape or gate_scales.shape != up_scales.shape
+            or gate_biases.shape != up_biases.shape or up_scales.dtype != values.dtype
+            or up_biases.dtype != values.dtype):
+        raise ValueError("affine SwiGLU requires matching gate/up weights and parameters")
+    _check_params(values, gate_weight, gate_scales, gate_biases, group_size, bits, "affine SwiGLU")
+    k = values.shape[-1]
+    n = gate_weight.shape[0]
+    lead = tuple(values.shape[:-1])
+    x = values.reshape(-1, k).contiguous()
+    m = x.shape[0]
+    out = torch.empty(*lead, n, dtype=values.dtype, device=values.device)
+    if m == 0:
+        return out
+    gw, uw = _as_u32(gate_weight), _as_u32(up_weight)
+    gs, gb = gate_scales.contiguous(), gate_biases.contiguous()
+    us, ub = up_scales.contiguous(), up_biases.contiguous()
+    L = _lib.lib()
+    need = L.mt_affine_qmv_workspace_bytes(m, k, n, group_size, bits, 2)
+    ws = workspace(values.device, need) if need else None
+    _lib.check(L.mt_affine_swiglu(
+        x.data_ptr(), gw.data_ptr(), gs.data_ptr(), gb.data_ptr(), uw.data_ptr(), us.data_ptr(),
+        ub.data_ptr(), out.data_ptr(), m, k, n, group_size, bits, code, _ptr(ws),
+        0 if ws is None else ws.numel(), _stream_handle(values.device)))
+    return out
+
+
+def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
+    """``down(swiglu(values)) (+ residual)`` in two kernels through one C-ABI call.
+
+    ``gate``/``up``/``down`` are ``(weight, scales, biases)`` triples; gate/up ``[I, H]``,
+    down ``[H, I]``. The hidden activation is rounded to the activation dtype between the two
+    kernels, as the reference executor does (``metile/backends/mlx_quantized.py:1829-1830``).
+    """
+    gw, gs, gb = gate
+    uw, us, ub = up
+    dw, ds, db = down
+    _require_device(values, gw, gs, gb, uw, us, ub, dw, ds, db, residual)
+    code = _dtype_code(values.dtype)
+    _check_params(values, gw, gs, gb, group_size, bits, "affine MLP gate")
+    _check_params(values, uw, us, ub, group_size, bits, "affine MLP up")
+    hdim = values.shape[-1]
+    idim = gw.shape[0]
+    if dw.shape[0] != hdim or dw.shape[1] * 32 // bits != idim:
+        raise ValueError("affine MLP received incompatible down-projection parameters")
+    if (tuple(ds.shape) != (hdim, idim // group_size) or tuple(db.shape) != tuple(ds.shape)
+            or ds.dtype != values.dtype or db.dtype != values.dtype):
+        raise ValueError("affine MLP received incompatible down-projection parameters")
+    lead = tuple(values.shape[:-1])
+    x = values.reshape(-1, hdim).contiguous()
+    m = x.shape[0]
+    out = torch.empty(*lead, hdim, dtype=values.dtype, device=values.device)
+    if m == 0:
+        return out
+    res = None
+    if residual is not None:
+        if tuple(residual.shape) != (*lead, hdim) or residual.dtype != values.dtype:
+            raise ValueError("residual must match the affine MLP output shape and dtype")
+        res = residual.reshape(m, hdim).contiguous()
+    tensors = [_as_u32(gw), gs.contiguous(), gb.contiguous(), _as_u32(uw), us.contiguous(),
+               ub.contiguous(), _as_u32(dw), ds.contiguous(), db.contiguous()]
+    L = _lib.lib()
+    need = L.mt_affine_mlp_workspace_bytes(m, hdim, idim, group_size, bits)
+    ws = workspace(values.device, need)
+    _lib.check(L.mt_affine_mlp(
+        x.data_ptr(), *[t.data_ptr() for t in tensors], _ptr(res), out.data_ptr(), m, hdim, idim,
+        group_size, bits, code, ws.data_ptr(), ws.numel(), _stream_handle(values.device)))
+    return out
+
+
+def affine_dequantize(weight, scales, biases, *, group_size=64, bits=4):
+    """Bit-exact fp32 ``q * s + b`` as a ``[N, K]`` float32 tensor
+    (``kernels/affine_qmv.py:41-51``)."""
+    _require_device(weight, scales, biases)
+    code = _dtype_code(scales.dtype)
+    if biases is None or biases.dtype != scales.dtype or biases.shape != scales.shape:
+        raise ValueError("dequantize requires biases matching the scales")
+    n = weight.shape[0]
+    k = weight.shape[1] * 32 // bits
+    out = torch.empty(n, k, dtype=torch.float32, device=weight.device)
+    w = _as_u32(weight)
+    s, b = scales.contiguous(), biases.contiguous()
+    _lib.check(_lib.lib().mt_affine_dequantize(
+        w.data_ptr(), s.data_ptr(), b.data_ptr(), out.data_ptr(), n, k, group_size, bits, code,
+        _stream_handle(weight.device)))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# reference-named entry points (metile/backends/mlx_quantized.py)
+# ---------------------------------------------------------------------------------------------
+
+
+def mlx_affine_qmv(values, weight, scales, biases, *, group_size=64, bits=4, block=32,
+                   outputs_per_simdgroup=1, decode_dtype="f32"):
+    """Drop-in for ``mlx_affine_qmv`` (``metile/backends/mlx_quantized.py:691-714``).
+
+    ``block``, ``outputs_per_simdgroup`` and ``decode_dtype`` choose among the reference's
+    Metal schedules; the gfx950 kernel has one schedule and always decodes exactly in fp32, so
+    they are validated and otherwise unused.
+    """
+    if block not in (32, 64, 128, 256) or outputs_per_simdgroup not in (1, 2, 4, 8):
+        raise ValueError("unsupported affine QMV schedule")
+    if decode_dtype not in ("f32", "f16"):
+        raise ValueError("decode_dtype must be 'f32' or 'f16'")
+    return affine_qmv(values, weight, scales, biases, group_size=group_size, bits=bits)
+
+
+def mlx_affine_residual_qmv(values, weight, scales, biases, residual, *, group_size=64, bits=4,
+                            autotune=True):
+    """Drop-in for ``mlx_affine_residual_qmv`` with the reference's guards
+    (``metile/backends/mlx_quantized.py:1538-1568``)."""
+    mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual,
+                                   group_size=group_size, bits=bits)
+    return affine_qmv(values, weight, scales, biases, group_size=group_size, bits=bits,
+                      residual=residual)
+
+
+def _swiglu_guards(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                   up_biases, group_size, bits):
+    if not ((bits == 4 and group_size == 64) or (bits == 8 and group_size in {32, 64, 128})):
+        raise ValueError("affine SwiGLU requires 4-bit group-64 or 8-bit group-32/64/128 weights")
+    if gate_biases is None or up_biases is None:
+        raise ValueError("affine SwiGLU requires affine quantization biases")
+    if (values.dtype != gate_scales.dtype or values.dtype != gate_biases.dtype
+            or gate_weight.shape != up_weight.shape or gate_scales.shape != up_scales.shape
+            or gate_biases.shape != up_biases.shape):
+        raise ValueError("affine SwiGLU requires matching gate/up weights and parameters")
+    if group_size % 64:
+        raise NotImplementedError(
+            "8-bit group-32 affine SwiGLU has no gfx950 kernel yet (groups of 64 and 128 do)")
+
+
+def mlx_affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                      up_biases, *, group_size=64, bits=4, autotune=True):
+    """Drop-in for ``mlx_affine_swiglu`` with the reference's guards
+    (``metile/backends/mlx_quantized.py:1645-1670``)."""
+    _swiglu_guards(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                   up_biases, group_size, bits)
+    return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                         up_biases, group_size=group_size, bits=bits)
+
+
+def mlx_affine_swiglu_qmv(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                          up_biases, *, group_size=64, bits=4, block=32, outputs_per_simdgroup=1,
+                          decode_dtype="f32"):
+    """Drop-in for the fixed-schedule ``mlx_affine_swiglu_qmv``
+    (``metile/backends/mlx_quantized.py:717-751``)."""
+    if block not in (32, 64, 128, 256) or outputs_per_simdgroup not in (1, 2, 4, 8):
+        raise ValueError("unsupported affine SwiGLU schedule")
+    return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                         up_biases, group_size=group_size, bits=bits)
+
+
+def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
+                               up_scales, up_biases, *, group_size=64, bits=4):
+    """Drop-in for ``mlx_affine_swiglu_executor`` (``metile/backends/mlx_quantized.py:1723``):
+    validates once and returns ``execute(values)`` bound to the weights."""
+    _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                   up_biases, group_size, bits)
+
+    def execute(values):
+        return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                             up_biases, group_size=group_size, bits=bits)
+
+    return execute
+
+
+def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
+                            up_scales, up_biases, down_weight, down_scales, down_biases,
+                            sample_residual, *, group_size=64, bits=4):
+    """Drop-in for ``mlx_affine_mlp_executor`` (``metile/backends/mlx_quantized.py:1770-1832``):
+    runs the SwiGLU and residual guards on the sample and returns
+    ``execute(values, residual) = down(swiglu(values)) + residual``."""
+    _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                   up_biases, group_size, bits)
+    hidden_shape = (*sample_values.shape[:-1], gate_weight.shape[0])
+    probe = torch.empty(hidden_shape, dtype=sample_values.dtype, device="meta")
+    mlx_affine_residual_qmv_guards(probe, down_weight, down_scales, down_biases, sample_residual,
+                                   group_size=group_size, bits=bits)
+    gate = (gate_weight, gate_scales, gate_biases)
+    up = (up_weight, up_scales, up_biases)
+    down = (down_weight, down_scales, down_biases)
+
+    def execute(values, residual):
+        return affine_mlp(values, gate, up, down, group_size=group_size, bits=bits,
+                          residual=residual)
+
+    return execute
+
+
+def mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual, *, group_size=64,
+                                   bits=4):
+    """The argument checks of ``mlx_affine_residual_qmv`` without running it."""
+    if group_size != 64 or bits != 4:
+        raise ValueError("affine residual QMV requires 4-bit weights with group size 64")
+    if biases is None:
+        raise ValueError("affine residual QMV requires affine quantization biases")
+    k = values.shape[-1]
+    n = weight.shape[0]
+    shape = (n, k // group_size)
+    if (weight.ndim != 2 or weight.shape[1] * 32 // bits != k or tuple(scales.shape) != shape
+            or tuple(biases.shape) != shape):
+        raise ValueError("affine residual QMV received incompatible quantization parameters")
+    if scales.dtype != values.dtype or biases.dtype != values.dtype:
+        raise ValueError("affine residual QMV parameters must match the input dtype")
+    if tuple(residual.shape) != (*values.shape[:-1], n) or residual.dtype != values.dtype:
+        raise ValueError("residual must match the affine QMV output shape and dtype")

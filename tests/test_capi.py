@@ -1,0 +1,54 @@
+"""The C-ABI library loads without a GPU and exports every function include/*.h declares."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from metile_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_functions() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(mt_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_header_declares_the_bound_signatures():
+    assert declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in sorted(declared_functions()) if not hasattr(handle, n)]
+    assert not missing, missing
+
+
+def test_version_and_error_reporting_without_gpu():
+    lib = _lib.lib()
+    assert lib.mt_version().decode().startswith("metile_amd")
+    # argument validation runs on the host, before any HIP call
+    st = lib.mt_affine_qmv(None, None, None, None, None, None, 1, 100, 64, 64, 4, 0, None, 0,
+                           None)
+    assert st == _lib.MT_ERR_INVALID_ARGUMENT
+    assert "group_size" in lib.mt_last_error().decode()
+    st = lib.mt_affine_qmv(None, None, None, None, None, None, 1, 128, 64, 64, 3, 0, None, 0,
+                           None)
+    assert st == _lib.MT_ERR_INVALID_ARGUMENT and "bits" in lib.mt_last_error().decode()
+
+
+def test_workspace_sizes_are_row_independent_plans():
+    lib = _lib.lib()
+    # split-K partials scale with rows (capped at one 32-row chunk), the plan does not change
+    w1 = lib.mt_affine_qmv_workspace_bytes(1, 8960, 1536, 64, 4, 1)
+    w32 = lib.mt_affine_qmv_workspace_bytes(32, 8960, 1536, 64, 4, 1)
+    w64 = lib.mt_affine_qmv_workspace_bytes(64, 8960, 1536, 64, 4, 1)
+    assert 0 < w1 < w32 == w64
+    assert lib.mt_affine_mlp_workspace_bytes(4, 1536, 8960, 64, 4) >= 4 * 8960 * 2
+    assert lib.mt_affine_qmv_workspace_bytes(1, 100, 64, 64, 4, 1) == 0  # invalid K

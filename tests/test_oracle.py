@@ -1,0 +1,259 @@
+"""Pins the NumPy oracle (CPU only) against known answers, closed forms, brute force and an
+independent implementation (torch CPU), so that a plausible mistake in it fails a test."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from oracle import affine as O
+
+
+# ---- bf16 rounding ------------------------------------------------------------------------
+
+
+def _torch_bf16_bits(f32: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(f32).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_bf16_rounding_matches_torch_on_edge_patterns():
+    rng = np.random.default_rng(0)
+    bits = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32)
+    # ties (low half exactly 0x8000) with both mantissa parities, denormals, infinities
+    ties = (rng.integers(0, 2**16, size=4096, dtype=np.uint32) << 16) | np.uint32(0x8000)
+    special = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x00000001, 0x007FFFFF,
+                        0x3F808000, 0x3F818000, 0x7F7FFFFF, 0x477FE000], dtype=np.uint32)
+    f = np.concatenate([bits, ties, special]).view(np.float32)
+    f = f[~np.isnan(f)]
+    np.testing.assert_array_equal(O.f32_to_bf16_bits(f), _torch_bf16_bits(f))
+
+
+def test_bf16_widening_is_exact():
+    b = np.arange(0, 2**16, dtype=np.uint32).astype(np.uint16)
+    f = O.bf16_bits_to_f32(b)
+    ok = ~np.isnan(f)
+    np.testing.assert_array_equal(O.f32_to_bf16_bits(f[ok]), b[ok])
+
+
+def test_half_ulp_bf16_known_values():
+    np.testing.assert_allclose(O.half_ulp(np.array([1.0, 1.5, 2.0, 255.0, 0.75])),
+                               [2**-8, 2**-8, 2**-7, 2**-1, 2**-9])
+
+
+# ---- packing ------------------------------------------------------------------------------
+
+
+def test_unpack_hand_built_words():
+    w = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.uint32)
+    np.testing.assert_array_equal(O.unpack_codes(w, 4)[0], np.arange(16))
+    w8 = np.array([[0x03020100, 0xFFFE8180]], dtype=np.uint32)
+    np.testing.assert_array_equal(O.unpack_codes(w8, 8)[0], [0, 1, 2, 3, 0x80, 0x81, 0xFE, 0xFF])
+
+
+def test_pack_hand_built_codes():
+    codes = np.arange(16, dtype=np.uint32)[None, :]
+    np.testing.assert_array_equal(O.pack_codes(codes, 4), [[0x76543210, 0xFEDCBA98]])
+
+
+@settings(max_examples=60, deadline=None)
+@given(bits=st.sampled_from([4, 8]), n=st.integers(1, 5), words=st.integers(1, 6),
+       seed=st.integers(0, 2**31))
+def test_pack_unpack_round_trip(bits, n, words, seed):
+    per = 32 // bits
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 1 << bits, size=(n, words * per), dtype=np.uint32)
+    packed = O.pack_codes(codes, bits)
+    assert packed.shape == (n, words)
+    np.testing.assert_array_equal(O.unpack_codes(packed, bits), codes)
+    raw = rng.integers(0, 2**32, size=(n, words), dtype=np.uint64).astype(np.uint32)
+    np.testing.assert_array_equal(O.pack_codes(O.unpack_codes(raw, bits), bits), raw)
+
+
+# ---- dequantization -----------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("bits,zero", [(4, 8.0), (8, 128.0)])
+def test_dequantize_closed_form_baseline_recipe(bits, zero):
+    w_q, s, b = O.make_affine_weight(48, 256, bits, 64, config_id=7, tensor_id=3)
+    got = O.dequantize(w_q, s, b, 64, bits)
+    q = O.unpack_codes(w_q, bits).astype(np.float64)
+    s64 = np.repeat(O.bf16_bits_to_f32(s).astype(np.float64), 64, axis=1)
+    expected = (q - zero) * s64  # exact: (q - zero) has <= 8 bits, s has 8
+    np.testing.assert_array_equal(got.astype(np.float64), expected)
+
+
+def _brute_force_qmv(x, w_q, s, b, k, group_size, bits):
+    """Literal loop of kernels/affine_qmv.py:32-53 (per word, per element), float64."""
+    per = 32 // bits
+    words_per_row = k // per
+    words_per_group = group_size // per
+    n = w_q.shape[0]
+    out = np.zeros((x.shape[0], n))
+    for row in range(x.shape[0]):
+        for col in range(n):
+            acc = 0.0
+            for wi in range(words_per_row):
+                packed = int(w_q[col, wi])
+                g = wi // words_per_group
+                scale = float(s[col, g])
+                bias = float(b[col, g])
+                for e in range(per):
+                    q = (packed >> (e * bits)) & ((1 << bits) - 1)
+                    acc += float(x[row, wi * per + e]) * (q * scale + bias)
+            out[row, col] = acc
+    return out
+
+
+@pytest.mark.parametrize("bits,group_size", [(4, 64), (8, 64), (4, 128), (8, 32)])
+def test_qmv_matches_brute_force_loop(bits, group_size):
+    k, n, m = 256, 6, 3
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 1 << bits, size=(n, k), dtype=np.uint32)
+    w_q = O.pack_codes(codes, bits)
+    s = O.f32_to_bf16_bits(rng.uniform(0.01, 0.1, size=(n, k // group_size)).astype(np.float32))
+    b = O.f32_to_bf16_bits(rng.uniform(-0.5, 0.5, size=(n, k // group_size)).astype(np.float32))
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    got = O.affine_qmv(x, w_q, s, b, group_size, bits)
+    ref = _brute_force_qmv(O.bf16_bits_to_f32(x), w_q, O.bf16_bits_to_f32(s),
+                           O.bf16_bits_to_f32(b), k, group_size, bits)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_reference_known_answer_seed_211():
+    """Restates tests/test_affine_quantized.py:120-163: seed 211, 64x64, f16, one group per
+    output row; the reference packs K-major nibble pairs, this oracle takes MLX output-major
+    words, so the codes are repacked and the reference's own fp32 expectation is compared."""
+    k = n = 64
+    random = np.random.default_rng(211)
+    activations = random.normal(size=(1, k)).astype(np.float16)
+    quantized = random.integers(0, 16, size=(n, k), dtype=np.uint8)
+    scales = random.uniform(0.01, 0.2, size=(1, n)).astype(np.float16)
+    biases = random.uniform(-0.5, 0.5, size=(1, n)).astype(np.float16)
+    expected_weight = (quantized.astype(np.float32) * scales.T.astype(np.float32)
+                       + biases.T.astype(np.float32))
+    expected = (activations.astype(np.float32) @ expected_weight.T).astype(np.float16)
+
+    w_q = O.pack_codes(quantized, 4)
+    got32 = O.affine_qmv(activations, w_q, scales.T.copy(), biases.T.copy(), 64, 4, dtype="f16",
+                         acc=np.float32)
+    np.testing.assert_array_equal(O.from_f32(got32.astype(np.float32), "f16"), expected)
+    np.testing.assert_array_equal(O.dequantize(w_q, scales.T.copy(), biases.T.copy(), 64, 4,
+                                               "f16"), expected_weight)
+
+
+def test_qmv_matches_torch_cpu_independent_path():
+    w_q, s, b = O.make_affine_weight(40, 512, 4, 64, config_id=1, tensor_id=10)
+    x = O.make_activations(5, 512, config_id=1)
+    got = O.affine_qmv(x, w_q, s, b, 64, 4)
+    # torch: unpack with int64 shifts, dequantize, fp64 matmul
+    wt = torch.from_numpy(w_q.astype(np.int64))
+    shifts = torch.arange(0, 32, 4, dtype=torch.int64)
+    q = ((wt[:, :, None] >> shifts) & 15).reshape(40, 512).double()
+    st_ = torch.from_numpy(s.view(np.int16)).view(torch.bfloat16).double()
+    bt = torch.from_numpy(b.view(np.int16)).view(torch.bfloat16).double()
+    w = q * st_.repeat_interleave(64, dim=1) + bt.repeat_interleave(64, dim=1)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).double()
+    np.testing.assert_allclose(got, (xt @ w.T).numpy(), rtol=1e-12, atol=1e-10)
+
+
+# ---- SwiGLU / MLP -------------------------------------------------------------------------
+
+
+def test_silu_mul_special_cases():
+    g = np.array([0.0, 60.0, -60.0, 1.0, -1.0])
+    u = np.array([3.0, 2.0, 2.0, 1.0, 1.0])
+    out = O.silu_mul(g, u)
+    assert out[0] == 0.0
+    assert out[1] == pytest.approx(120.0)
+    assert abs(out[2]) < 1e-20
+    ref = torch.nn.functional.silu(torch.tensor(g)) * torch.tensor(u)
+    np.testing.assert_allclose(out, ref.numpy(), rtol=1e-12)
+    with np.errstate(over="raise"):
+        pass
+    assert np.isfinite(O.silu_mul(np.array([-1e4]), np.array([1.0]))).all()
+
+
+def test_mlp_composition_matches_torch_cpu():
+    h, i, m = 128, 192, 3
+    gate = O.make_affine_weight(i, h, 4, 64, 1, 10)
+    up = O.make_affine_weight(i, h, 4, 64, 1, 12)
+    down = O.make_affine_weight(h, i, 4, 64, 1, 14)
+    x = O.make_activations(m, h, 1)
+    res = O.make_activations(m, h, 1, tensor_id=3)
+    y, hid = O.affine_mlp(x, gate, up, down, 64, 4, residual=res)
+
+    def deq(t):
+        return torch.from_numpy(O.dequantize(*t, 64, 4).astype(np.float64))
+
+    xt = torch.from_numpy(O.bf16_bits_to_f32(x).astype(np.float64))
+    hh = torch.nn.functional.silu(xt @ deq(gate).T) * (xt @ deq(up).T)
+    hh_b = hh.float().to(torch.bfloat16)
+    np.testing.assert_array_equal(hid, hh_b.view(torch.int16).numpy().view(np.uint16))
+    yt = hh_b.double() @ deq(down).T + torch.from_numpy(O.bf16_bits_to_f32(res).astype(np.float64))
+    np.testing.assert_allclose(y, yt.numpy(), rtol=1e-12, atol=1e-10)
+
+
+# ---- dense typed rounding -----------------------------------------------------------------
+
+
+def test_dense_swiglu_matches_torch_typed_ops():
+    k, n, m = 256, 64, 4
+    x = O.make_activations(m, k, 2)
+    g = O.make_dense_weight(n, k, 2, 10)
+    u = O.make_dense_weight(n, k, 2, 11)
+    got = O.dense_swiglu(x, g, u)
+
+    def tb(a):
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+
+    xt = tb(x).double()
+    left = (xt @ tb(g).double().T).float().to(torch.bfloat16)
+    right = (xt @ tb(u).double().T).float().to(torch.bfloat16)
+    y = 1 / (1 + torch.exp(left.abs()))          # each op rounds to bf16 on torch CPU
+    sig = torch.where(left < 0, y, 1 - y)
+    act = left * sig
+    out = act * right
+    np.testing.assert_array_equal(got, out.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_dense_residual_rounds_projection_then_sum():
+    k, n, m = 128, 32, 3
+    x = O.make_activations(m, k, 2)
+    w = O.make_dense_weight(n, k, 2, 12)
+    r = O.make_activations(m, n, 2, tensor_id=3)
+    got = O.dense_residual_qmv(x, w, r)
+
+    def tb(a):
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+
+    proj = (tb(x).double() @ tb(w).double().T).float().to(torch.bfloat16)
+    out = proj + tb(r)
+    np.testing.assert_array_equal(got, out.view(torch.int16).numpy().view(np.uint16))
+
+
+# ---- tolerance metric ---------------------------------------------------------------------
+
+
+def test_tolerance_metric_catches_planted_mistakes():
+    w_q, s, b = O.make_affine_weight(64, 512, 4, 64, 0, 1)
+    x = O.make_activations(2, 512, 0)
+    ref = O.affine_qmv(x, w_q, s, b, 64, 4)
+    exact = O.from_f32(ref.astype(np.float32), "bf16")
+    assert O.tolerance_error(exact, ref) == 0.0
+    # dropped bias term
+    no_bias = O.affine_qmv(x, w_q, s, np.zeros_like(b), 64, 4)
+    assert O.tolerance_error(O.from_f32(no_bias.astype(np.float32), "bf16"), ref) > 1e-1
+    # transposed / misindexed weight: shuffled output columns
+    perm = O.from_f32(ref[:, ::-1].astype(np.float32), "bf16")
+    assert O.tolerance_error(perm, ref) > 1e-1
+    # one-ulp perturbation of a mid-size element stays within the contract
+    bumped = exact.copy()
+    bumped[0, 3] += 1
+    assert O.tolerance_error(bumped, ref) < 2e-3 * 4
+
+
+def test_algorithmic_bytes_config0():
+    assert O.algorithmic_bytes_affine(1, 1536, 8960, 4, 64) == 7_762_432
