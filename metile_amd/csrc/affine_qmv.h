@@ -6,9 +6,9 @@
 
 namespace mt {
 
-// Largest number of 64-wide K steps one workgroup of the small-row kernel handles (bounds the
-// per-step activation sums kept in LDS). Larger K is split across workgroups.
-constexpr int kMaxStepsPerSplit = 64;
+// Largest number of quantization groups one workgroup of the small-row kernel covers (bounds
+// the scales and biases it stages in LDS). The host splits K so that this holds.
+constexpr int kMaxGroupsPerSplit = 64;
 
 struct QmvParams {
   const uint16_t* x;         // [M, K] activations
@@ -20,6 +20,7 @@ struct QmvParams {
   float* partial;            // [ksplit][nproj][M][N] split-K partial sums
   uint32_t* counters;        // [N/32] split-K arrival counters, zero between calls
   int M, K, N, G;
+  int group_shift;           // log2(G / 64)
   int ksplit;
   int steps_per_split;
 };

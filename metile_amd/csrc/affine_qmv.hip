@@ -5,17 +5,25 @@
 // of kernels/affine_qmv.py:124-132,204-214), reading every packed weight byte from HBM once
 // per dispatch whatever the row count.
 //
-// Design (wave64, MFMA 32x32x16):
-//  * A workgroup owns a strip of 32 output columns (32 gate + 32 up columns for SwiGLU) and a
-//    contiguous range of 64-wide K steps; its four waves split that range.
-//  * Per K step a lane (j, h) = (lane % 32, lane / 32) loads 32 consecutive K of column j
-//    (16 B of 4-bit codes or 32 B of 8-bit codes) and 32 consecutive activations of row j.
-//    Codes are turned into exact 16-bit floats (offset + q) in registers and multiplied by the
-//    activations on the matrix cores; rows >= M read as zero (buffer range check).
-//  * The per-group affine terms are applied to each step's fp32 MFMA result:
-//      acc += s * sum_k x_k (offset + q_k) + (b - offset * s) * sum_k x_k,
-//    which equals sum_k x_k (q_k s + b) exactly in real arithmetic. The per-row activation
-//    sums of each step are computed once per workgroup into LDS.
+// Design (wave64, MFMA 32x32x16, streaming):
+//  * A workgroup owns a strip of 32 output columns (for SwiGLU the same 32 gate and 32 up
+//    columns) and a range of 64-wide K steps; its four waves split the range into contiguous
+//    sub-ranges.
+//  * Per K step a lane (j, h) = (lane % 32, lane / 32) needs 32 consecutive K of column j
+//    (one 16-byte load of 4-bit codes, two of 8-bit codes; the two halves of a wave read the
+//    step's 32 or 64 contiguous bytes of each column) and 32 consecutive activations of row j.
+//    One step's loads form a pipeline stage; each wave keeps kStages stages in flight in
+//    registers and refills a stage as soon as it is consumed. A stage's loads are issued
+//    together, so waiting for one stage never waits for a later one (vector loads complete in
+//    issue order).
+//  * The group scales and biases of the workgroup's strip and K range are staged once into LDS
+//    with coalesced loads (issued before the weight prefetch) and read from there per step.
+//  * Codes are turned into exact 16-bit floats (offset + q) in registers and multiplied by the
+//    activations on the matrix cores. The per-group affine terms are applied to each step's
+//    fp32 MFMA result:  acc += s * sum_k x_k (offset + q_k) + (b - offset * s) * sum_k x_k.
+//    The per-row activation sums come from four more MFMAs of the same activations against a
+//    matrix of ones, which lands them in the accumulator layout directly.
+//  * Rows >= M and steps past the range read as zero through the buffer range check.
 //  * Cross-wave partials are reduced in LDS in a fixed order. When K is split across
 //    workgroups, fp32 partials go to a caller-provided workspace and the last workgroup of a
 //    strip (detected with a device-scope counter that it resets) sums them in split order and
@@ -27,154 +35,181 @@ namespace mt {
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kUnroll = 4;  // K steps in flight per wave
+template <int DT>
+__device__ __forceinline__ u32x4 ones8() {
+  constexpr uint32_t one2 = (DT == kBF16) ? 0x3F803F80u : 0x3C003C00u;
+  return (u32x4){one2, one2, one2, one2};
+}
 
-template <int BITS, int DT, int MROWS, int NPROJ>
-__global__ __launch_bounds__(kThreads) void affine_qmv_kernel(const QmvParams p) {
-  constexpr int kRegs = MROWS / 2;                  // valid accumulator registers per lane
-  constexpr int kWV = (BITS == 4) ? 1 : 2;          // 16-byte weight vectors per lane per step
+// One pipeline stage: the codes (16 B per 32 K of 4-bit, 32 B of 8-bit) of every projection
+// and the four 16-byte activation fragments of one K step.
+template <int BITS, int NPROJ>
+struct Stage {
+  u32x4 w[NPROJ][BITS / 4];
+  u32x4 x[4];
+};
+
+// B operand of MFMA e (K slice [8e, 8e+8) of the lane's 32 K) as 8 exact 16-bit floats.
+template <int BITS, int DT>
+__device__ __forceinline__ u32x4 bfrag(const u32x4 (&w)[BITS / 4], int e) {
+  if constexpr (BITS == 4) {
+    return unpack_u4<DT>(w[0][e]);
+  } else {
+    const u32x4 src = w[e >> 1];
+    const u32x2 lo = unpack_u8<DT>((e & 1) ? src.z : src.x);
+    const u32x2 hi = unpack_u8<DT>((e & 1) ? src.w : src.y);
+    return (u32x4){lo.x, lo.y, hi.x, hi.y};
+  }
+}
+
+// LDS row (in 32-bit words) of one column's scales or biases over a split's groups.
+constexpr int kSbRowWords = kMaxGroupsPerSplit / 2 + 2;
+
+template <int BITS, int DT, int MROWS, int NPROJ, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams p) {
+  constexpr int kThreads = WAVES * 64;
   constexpr float kOff = CodeOffset<BITS, DT>::value;
+  constexpr int kRegs = MROWS / 2;  // accumulator registers holding rows < MROWS
+  constexpr int kArrays = 2 * NPROJ;  // scales and biases of each projection
 
-  __shared__ __attribute__((aligned(16))) float xsum[kMaxStepsPerSplit][MROWS];
-  __shared__ float red[kWaves][NPROJ][MROWS][33];
+  __shared__ float red[WAVES][NPROJ][MROWS][33];
+  __shared__ uint32_t sb[kArrays][32][kSbRowWords];
   __shared__ int last_flag;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 31;
   const int h = lane >> 5;
   const int strip = blockIdx.x;
   const int split = blockIdx.y;
   const int M = p.M, K = p.K, N = p.N;
-  const int col = strip * 32 + j;
   const int steps_total = K >> 6;
   const int s_beg = split * p.steps_per_split;
   const int s_end = min(steps_total, s_beg + p.steps_per_split);
-  const int ns = s_end - s_beg;
-
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
-
-  // ---- per-row activation sums of every K step of this split --------------------------
-  for (int pp = tid; pp < ns * MROWS; pp += kThreads) {
-    const int sl = pp / MROWS;
-    const int m = pp - sl * MROWS;
-    float acc = 0.0f;
-    if (m < M) {
-      const uint32_t base = ((uint32_t)m * K + (uint32_t)(s_beg + sl) * 64u) * 2u;
-#pragma unroll
-      for (int v = 0; v < 8; ++v) acc = sum8<DT>(load16(rx, base + 16u * v), acc);
-    }
-    xsum[sl][m] = acc;
-  }
-  __syncthreads();
-
-  // ---- main loop --------------------------------------------------------------------------
-  const int per_wave = (ns + kWaves - 1) / kWaves;
+  const int per_wave = (s_end - s_beg + WAVES - 1) / WAVES;
   const int w_beg = s_beg + wave * per_wave;
   const int w_end = min(s_end, w_beg + per_wave);
+  const int gshift = p.group_shift;  // log2(G / 64)
+  // Scale rows are staged from the 32-bit word holding group g_beg; a row whose element
+  // index (row * groups_per_row + g_beg) is odd starts one 16-bit element into its segment.
+  const int g_beg = s_beg >> gshift;
+  const int g_last = (s_end - 1) >> gshift;
+  const int nwords = (g_last - g_beg + 1) / 2 + 1;  // 32-bit words per staged row segment
 
-  const int words_per_row = K * BITS / 32;
+  const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
   const int groups_per_row = K / p.G;
-  __amdgpu_buffer_rsrc_t rw[NPROJ], rs[NPROJ], rb[NPROJ];
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  __amdgpu_buffer_rsrc_t rw[NPROJ];
 #pragma unroll
-  for (int q = 0; q < NPROJ; ++q) {
-    rw[q] = make_rsrc(p.w[q], (uint32_t)N * words_per_row * 4u);
-    rs[q] = make_rsrc(p.s[q], (uint32_t)N * groups_per_row * 2u);
-    rb[q] = make_rsrc(p.b[q], (uint32_t)N * groups_per_row * 2u);
-  }
-  const uint32_t w_row = (uint32_t)col * words_per_row * 4u;       // byte offset of the row
-  const uint32_t g_row = (uint32_t)col * groups_per_row * 2u;
-  const uint32_t x_row = (j < M) ? (uint32_t)j * K * 2u : kOOB;
-  const int steps_per_group = p.G >> 6;
+  for (int pr = 0; pr < NPROJ; ++pr) rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * row_bytes);
 
-  f32x16 acc[NPROJ];
+  // ---- scales and biases of this strip and K range: issued first, parked in LDS below -----
+  // For each array (unrolled, so the buffer descriptor stays wave-uniform) thread t copies
+  // 16-byte quads q = t / 32 + k * (kThreads / 32) of row t % 32.
+  constexpr int kQuadsPerRow = (kSbRowWords + 3) / 4;
+  constexpr int kSbIters = (kQuadsPerRow + kThreads / 32 - 1) / (kThreads / 32);
+  const int sb_row = tid & 31;
+  const int sb_q0 = tid >> 5;
+  u32x4 sbv[kArrays][kSbIters];
 #pragma unroll
-  for (int q = 0; q < NPROJ; ++q) acc[q] = (f32x16){0};
-
-  for (int s0 = w_beg; s0 < w_end; s0 += kUnroll) {
-    u32x4 wv[kUnroll][NPROJ][kWV];
-    uint32_t sv[kUnroll][NPROJ], bv[kUnroll][NPROJ];
-    u32x4 xa[kUnroll][4];
+  for (int a = 0; a < kArrays; ++a) {
+    const uint16_t* src = (a & 1) ? p.b[a >> 1] : p.s[a >> 1];
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)N * groups_per_row * 2u);
+    const uint32_t base = (((uint32_t)(strip * 32 + sb_row) * groups_per_row + g_beg) * 2u) & ~3u;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int st = s0 + u;
-      const bool ok = st < w_end;
-      // 32 K of this lane's half-step: byte offset (64*st + 32*h) * BITS / 8.
-      const uint32_t woff = ok ? w_row + (uint32_t)(st * 64 + 32 * h) * BITS / 8u : kOOB;
-      const uint32_t goff = ok ? g_row + (uint32_t)(st / steps_per_group) * 2u : kOOB;
-#pragma unroll
-      for (int q = 0; q < NPROJ; ++q) {
-#pragma unroll
-        for (int v = 0; v < kWV; ++v) wv[u][q][v] = load16(rw[q], woff + 16u * v);
-        sv[u][q] = load2(rs[q], goff);
-        bv[u][q] = load2(rb[q], goff);
-      }
-      const uint32_t xoff = (ok && x_row != kOOB) ? x_row + (uint32_t)(st * 64 + 32 * h) * 2u
-                                                  : kOOB;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xa[u][e] = load16(rx, xoff == kOOB ? kOOB : xoff + 16u * e);
+    for (int k = 0; k < kSbIters; ++k) {
+      const int q = sb_q0 + k * (kThreads / 32);
+      sbv[a][k] = load16(r, 4 * q < nwords ? base + 16u * q : kOOB);
     }
+  }
+
+  // ---- weight and activation pipeline ----------------------------------------------------
+  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + (uint32_t)h * 4u * BITS;
+  const uint32_t x_row = j < M ? ((uint32_t)j * K + 32u * h) * 2u : kOOB;
+
+  Stage<BITS, NPROJ> ring[STAGES];
+  // Steps past this wave's range load nothing (range-checked offsets), so the refills below
+  // need no branch and every wait stays exact.
+  auto load_stage = [&](Stage<BITS, NPROJ>& S, int st) {
+    const bool ok = st < w_end;
+    const uint32_t woff = ok ? w_row + (uint32_t)st * 8u * BITS : kOOB;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int sl = s0 + u - s_beg;
-      float xs[kRegs];
-      if (s0 + u < w_end) {
+    for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-        for (int r4 = 0; r4 < kRegs / 4; ++r4) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(&xsum[sl][8 * r4 + 4 * h]);
-          xs[4 * r4 + 0] = v.x;
-          xs[4 * r4 + 1] = v.y;
-          xs[4 * r4 + 2] = v.z;
-          xs[4 * r4 + 3] = v.w;
-        }
-      } else {
+      for (int v = 0; v < BITS / 4; ++v)
+        S.w[pr][v] = load16(rw[pr], ok ? woff + 16u * v : kOOB);
+    const bool xok = ok && x_row != kOOB;
+    const uint32_t xoff = x_row + (uint32_t)st * 128u;
 #pragma unroll
-        for (int r = 0; r < kRegs; ++r) xs[r] = 0.0f;
-      }
+    for (int e = 0; e < 4; ++e) S.x[e] = load16(rx, xok ? xoff + 16u * e : kOOB);
+  };
 #pragma unroll
-      for (int q = 0; q < NPROJ; ++q) {
-        f32x16 t = (f32x16){0};
+  for (int d = 0; d < STAGES; ++d) load_stage(ring[d], w_beg + d);
+
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          u32x4 bfrag;
-          if constexpr (BITS == 4) {
-            const uint32_t word = (e == 0)   ? wv[u][q][0].x
-                                  : (e == 1) ? wv[u][q][0].y
-                                  : (e == 2) ? wv[u][q][0].z
-                                             : wv[u][q][0].w;
-            bfrag = unpack_u4<DT>(word);
-          } else {
-            const u32x4 src = wv[u][q][e >> 1];
-            const uint32_t w0 = (e & 1) ? src.z : src.x;
-            const uint32_t w1 = (e & 1) ? src.w : src.y;
-            const u32x2 lo = unpack_u8<DT>(w0);
-            const u32x2 hi = unpack_u8<DT>(w1);
-            bfrag = (u32x4){lo.x, lo.y, hi.x, hi.y};
+  for (int a = 0; a < kArrays; ++a)
+#pragma unroll
+    for (int k = 0; k < kSbIters; ++k) {
+      const int q = sb_q0 + k * (kThreads / 32);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (4 * q + c < kSbRowWords) sb[a][sb_row][4 * q + c] = sbv[a][k][c];
+    }
+  __syncthreads();
+
+  float acc[NPROJ][kRegs];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r) acc[pr][r] = 0.0f;
+
+  const u32x4 ones = ones8<DT>();
+  const f32x16 zero16 = (f32x16){0};
+  const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(&sb[0][0][0]);
+  const int sb_shift = ((strip * 32 + j) * groups_per_row + g_beg) & 1;
+  for (int s0 = w_beg; s0 < w_end; s0 += STAGES) {
+#pragma unroll
+    for (int d = 0; d < STAGES; ++d) {
+      Stage<BITS, NPROJ>& S = ring[d];
+      const int st = s0 + d;
+      if (st < w_end) {
+        f32x16 xs = mfma32<DT>(S.x[0], ones, zero16);
+#pragma unroll
+        for (int e = 1; e < 4; ++e) xs = mfma32<DT>(S.x[e], ones, xs);
+        const int gl = (st >> gshift) - g_beg + sb_shift;
+#pragma unroll
+        for (int pr = 0; pr < NPROJ; ++pr) {
+          f32x16 t = mfma32<DT>(S.x[0], bfrag<BITS, DT>(S.w[pr], 0), zero16);
+#pragma unroll
+          for (int e = 1; e < 4; ++e) t = mfma32<DT>(S.x[e], bfrag<BITS, DT>(S.w[pr], e), t);
+          const float sf = act_to_f32<DT>(sb16[((2 * pr) * 32 + j) * 2 * kSbRowWords + gl]);
+          const float bf = act_to_f32<DT>(sb16[((2 * pr + 1) * 32 + j) * 2 * kSbRowWords + gl]);
+          const float bp = __builtin_fmaf(-kOff, sf, bf);
+#pragma unroll
+          for (int r = 0; r < kRegs; ++r) {
+            acc[pr][r] = __builtin_fmaf(sf, t[r], acc[pr][r]);
+            acc[pr][r] = __builtin_fmaf(bp, xs[r], acc[pr][r]);
           }
-          t = mfma32<DT>(xa[u][e], bfrag, t);
-        }
-        const float sf = act_to_f32<DT>(sv[u][q]);
-        const float bf = act_to_f32<DT>(bv[u][q]);
-        const float bp = __builtin_fmaf(-kOff, sf, bf);
-#pragma unroll
-        for (int r = 0; r < kRegs; ++r) {
-          acc[q][r] = __builtin_fmaf(sf, t[r], acc[q][r]);
-          acc[q][r] = __builtin_fmaf(bp, xs[r], acc[q][r]);
         }
       }
+      load_stage(S, st + STAGES);
     }
   }
 
   // ---- cross-wave reduction (fixed order) --------------------------------------------------
 #pragma unroll
-  for (int q = 0; q < NPROJ; ++q) {
+  for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-    for (int r = 0; r < kRegs; ++r) red[wave][q][mfma32_row(r, h)][j] = acc[q][r];
-  }
+    for (int r = 0; r < kRegs; ++r) red[wave][pr][mfma32_row(r, h)][j] = acc[pr][r];
   __syncthreads();
+
+  auto reduce = [&](int pr, int i, int c) {
+    float v = red[0][pr][i][c];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += red[w][pr][i][c];
+    return v;
+  };
 
   const int outs = M * 32;
   if (p.ksplit == 1) {
@@ -182,8 +217,7 @@ __global__ __launch_bounds__(kThreads) void affine_qmv_kernel(const QmvParams p)
       const int i = o >> 5, c = o & 31;
       float v[NPROJ];
 #pragma unroll
-      for (int q = 0; q < NPROJ; ++q)
-        v[q] = ((red[0][q][i][c] + red[1][q][i][c]) + red[2][q][i][c]) + red[3][q][i][c];
+      for (int pr = 0; pr < NPROJ; ++pr) v[pr] = reduce(pr, i, c);
       const size_t oi = (size_t)i * N + strip * 32 + c;
       float out;
       if constexpr (NPROJ == 2) {
@@ -206,9 +240,9 @@ __global__ __launch_bounds__(kThreads) void affine_qmv_kernel(const QmvParams p)
   for (int o = tid; o < outs; o += kThreads) {
     const int i = o >> 5, c = o & 31;
 #pragma unroll
-    for (int q = 0; q < NPROJ; ++q) {
-      const float v = ((red[0][q][i][c] + red[1][q][i][c]) + red[2][q][i][c]) + red[3][q][i][c];
-      __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + q) * plane + (size_t)i * N +
+    for (int pr = 0; pr < NPROJ; ++pr) {
+      const float v = reduce(pr, i, c);
+      __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + pr) * plane + (size_t)i * N +
                                     strip * 32 + c],
                          v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -227,12 +261,12 @@ __global__ __launch_bounds__(kThreads) void affine_qmv_kernel(const QmvParams p)
     const size_t oi = (size_t)i * N + strip * 32 + c;
     float v[NPROJ];
 #pragma unroll
-    for (int q = 0; q < NPROJ; ++q) {
+    for (int pr = 0; pr < NPROJ; ++pr) {
       float sacc = 0.0f;
       for (int sp = 0; sp < p.ksplit; ++sp)
-        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + q) * plane + oi],
+        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + pr) * plane + oi],
                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[q] = sacc;
+      v[pr] = sacc;
     }
     float out;
     if constexpr (NPROJ == 2) {
@@ -247,18 +281,31 @@ __global__ __launch_bounds__(kThreads) void affine_qmv_kernel(const QmvParams p)
     __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Pipeline depth: as many K steps in flight per wave as fit in about 128 registers.
+template <int BITS, int NPROJ, int MROWS>
+constexpr int stages() {
+  constexpr int per_stage = NPROJ * BITS + 16;  // registers of one stage
+  constexpr int s = 128 / per_stage - (MROWS == 32 ? 1 : 0);
+  return s < 2 ? 2 : s;
+}
+
+template <int BITS, int DT, int MROWS, int NPROJ>
+hipError_t launch_waves(const QmvParams& p, hipStream_t stream) {
+  // Four waves per workgroup, so that two or three workgroups fit on a CU and a grid of a
+  // few hundred workgroups is resident at once (a workgroup that waits for a free CU doubles
+  // the kernel time of a weight-streaming launch).
+  constexpr int kW = 4;
+  const dim3 grid(p.N / 32, p.ksplit);
+  affine_qmv_kernel<BITS, DT, MROWS, NPROJ, kW, stages<BITS, NPROJ, MROWS>()>
+      <<<grid, dim3(kW * 64), 0, stream>>>(p);
+  return hipGetLastError();
+}
+
 template <int BITS, int DT, int NPROJ>
 hipError_t launch_rows(const QmvParams& p, hipStream_t stream) {
-  const dim3 grid(p.N / 32, p.ksplit);
-  const dim3 block(kThreads);
-  if (p.M <= 8) {
-    affine_qmv_kernel<BITS, DT, 8, NPROJ><<<grid, block, 0, stream>>>(p);
-  } else if (p.M <= 16) {
-    affine_qmv_kernel<BITS, DT, 16, NPROJ><<<grid, block, 0, stream>>>(p);
-  } else {
-    affine_qmv_kernel<BITS, DT, 32, NPROJ><<<grid, block, 0, stream>>>(p);
-  }
-  return hipGetLastError();
+  if (p.M <= 8) return launch_waves<BITS, DT, 8, NPROJ>(p, stream);
+  if (p.M <= 16) return launch_waves<BITS, DT, 16, NPROJ>(p, stream);
+  return launch_waves<BITS, DT, 32, NPROJ>(p, stream);
 }
 
 template <int BITS, int DT>

@@ -34,9 +34,8 @@ constexpr int kRowChunk = 32;  // rows per small-row dispatch
 constexpr size_t kCounterBytes = 64 * 1024;
 constexpr int kMaxStrips = (int)(kCounterBytes / 4);
 
-// Split-K plan of the small-row kernel for one (K, N): enough workgroups to cover the chip
-// about twice, at least four K steps per split, and no split longer than kMaxStepsPerSplit.
-// Depends only on K and N, never on the row count.
+// Split-K plan of the small-row kernel for one (K, N): about 1.5 workgroups per CU, with at
+// least 16 K steps (4 per wave) in each split. Depends only on K and N.
 struct Plan {
   int ksplit;
   int steps_per_split;
@@ -45,10 +44,11 @@ struct Plan {
 Plan plan_qmv(int K, int N) {
   const int steps = K / 64;
   const int strips = N / 32;
-  int ksplit = (512 + strips - 1) / strips;
-  const int max_split = steps / 4 > 0 ? steps / 4 : 1;
+  int ksplit = (384 + strips / 2) / strips;
+  const int max_split = steps / 16 > 0 ? steps / 16 : 1;
   if (ksplit > max_split) ksplit = max_split;
-  const int min_split = (steps + mt::kMaxStepsPerSplit - 1) / mt::kMaxStepsPerSplit;
+  // Each split covers at most kMaxGroupsPerSplit - 1 groups of 64 (one more may straddle).
+  const int min_split = (steps + mt::kMaxGroupsPerSplit - 2) / (mt::kMaxGroupsPerSplit - 1);
   if (ksplit < min_split) ksplit = min_split;
   if (const char* env = std::getenv("METILE_AMD_KSPLIT")) {
     const int forced = std::atoi(env);
@@ -75,9 +75,9 @@ int check_affine(const char* op, int M, int K, int N, int group_size, int bits, 
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": dtype must be MT_BF16 or MT_F16");
   if (M < 1 || K < 1 || N < 1)
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": M, K and N must be positive");
-  if (group_size < 64 || group_size % 64 || K % group_size)
+  if (group_size < 64 || (group_size & (group_size - 1)) || K % group_size)
     return fail(MT_ERR_INVALID_ARGUMENT,
-                std::string(op) + ": group_size must be a multiple of 64 that divides K");
+                std::string(op) + ": group_size must be a power of two >= 64 that divides K");
   if (K % 64 || N % 32)
     return fail(MT_ERR_INVALID_ARGUMENT,
                 std::string(op) + ": K must be a multiple of 64 and N a multiple of 32");
@@ -127,6 +127,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.K = K;
     p.N = N;
     p.G = group_size;
+    p.group_shift = __builtin_ctz((unsigned)(group_size / 64));
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
     const hipError_t e = mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
