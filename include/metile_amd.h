@@ -86,6 +86,29 @@ int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* bi
                          float* out, int N, int K, int group_size, int bits, int dtype,
                          void* stream);
 
+/* ---- dense 16-bit small-batch projections ------------------------------------------------ */
+
+/* Workspace bytes mt_dense_swiglu (nproj = 2) or mt_dense_residual_qmv (nproj = 1) needs. */
+size_t mt_dense_workspace_bytes(int M, int K, int N, int nproj);
+
+/* h = typed SwiGLU of x @ gate^T and x @ up^T, gate/up [N, K] 16-bit weights: the fp32 dots
+ * are rounded to the activation type, then silu and the product are evaluated with every
+ * operation rounded to that type (metile/compiler/dense.py:193-299 with
+ * metile/codegen/msl_emitter.py:1218-1252; entry mlx_dense_swiglu,
+ * metile/backends/mlx_dense_swiglu.py:424-491). Each output row is bit-identical whatever
+ * M is. K % 64 == 0, N % 32 == 0. */
+int mt_dense_swiglu(const void* x, const void* gate_w, const void* up_w, void* h, int M, int K,
+                    int N, int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* y = T(T(x @ w^T) + residual) (or T(x @ w^T) with a null residual), w [N, K]: the projected
+ * value is rounded to the activation type T before the residual add
+ * (metile/compiler/dense.py:302-381, metile/codegen/msl_emitter.py:1098-1120; entry
+ * mlx_dense_residual_qmv, metile/backends/mlx_dense_residual.py:276-319). Each output row is
+ * bit-identical whatever M is. */
+int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, void* y, int M,
+                          int K, int N, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,11 +1,12 @@
 """metile_amd — MI355X (gfx950) kernels for meTile's quantized-projection hot path.
 
-Affine 4/8-bit quantized QMV, fused SwiGLU and the quantized MLP, written as hand-written HIP
-kernels behind a C ABI (``include/metile_amd.h``) and exposed here on torch tensors with the
+Affine 4/8-bit quantized QMV, fused SwiGLU, the quantized MLP and dense 16-bit small-batch
+projections, written as hand-written HIP kernels behind a C ABI (``include/metile_amd.h``) and exposed here on torch tensors with the
 reference's call surface (``metile/backends/mlx_quantized.py``).
 """
 
 from ._lib import MetileError, version
+from .dense import DenseWeight, dense_qmv, dense_swiglu, mlx_dense_residual_qmv, mlx_dense_swiglu
 from .quantized import (
     affine_dequantize,
     affine_mlp,
@@ -20,7 +21,12 @@ from .quantized import (
 )
 
 __all__ = [
+    "DenseWeight",
     "MetileError",
+    "dense_qmv",
+    "dense_swiglu",
+    "mlx_dense_residual_qmv",
+    "mlx_dense_swiglu",
     "affine_dequantize",
     "affine_mlp",
     "affine_qmv",

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "affine_qmv.h"
+#include "dense_qmv.h"
 
 namespace {
 
@@ -136,6 +137,66 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
   return MT_OK;
 }
 
+constexpr int kDenseRowChunk = 128;  // rows per dense dispatch
+
+size_t dense_workspace(int M, int K, int N, int nproj) {
+  const Plan plan = plan_qmv(K, N);
+  if (plan.ksplit <= 1) return 0;
+  const int rows = M < kDenseRowChunk ? M : kDenseRowChunk;
+  return kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+}
+
+int check_dense(const char* op, int M, int K, int N, int dtype) {
+  if (dtype != MT_BF16 && dtype != MT_F16)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": dtype must be MT_BF16 or MT_F16");
+  if (M < 1 || K < 1 || N < 1)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": M, K and N must be positive");
+  if (K % 64 || N % 32)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": K must be a multiple of 64 and N a multiple of 32");
+  if (N / 32 > kMaxStrips)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": N larger than " +
+                                             std::to_string(kMaxStrips * 32) + " is unsupported");
+  if ((size_t)N * K * 2 >= (1ull << 31) || (size_t)kDenseRowChunk * K * 2 >= (1ull << 31))
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": tensor larger than 2 GiB");
+  return MT_OK;
+}
+
+int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
+              const void* residual, void* y, int M, int K, int N, int dtype, void* workspace,
+              size_t workspace_bytes, void* stream) {
+  int st = check_dense(op, M, K, N, dtype);
+  if (st) return st;
+  if (!x || !y) return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null x or output");
+  for (int q = 0; q < nproj; ++q)
+    if (!w[q]) return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null weight");
+  const size_t need = dense_workspace(M, K, N, nproj);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
+                                      " bytes required, got " + std::to_string(workspace_bytes));
+  const Plan plan = plan_qmv(K, N);
+  for (int r0 = 0; r0 < M; r0 += kDenseRowChunk) {
+    const int rows = (M - r0) < kDenseRowChunk ? (M - r0) : kDenseRowChunk;
+    mt::DenseParams p{};
+    p.x = static_cast<const uint16_t*>(x) + (size_t)r0 * K;
+    for (int q = 0; q < nproj; ++q) p.w[q] = static_cast<const uint16_t*>(w[q]);
+    p.residual = residual ? static_cast<const uint16_t*>(residual) + (size_t)r0 * N : nullptr;
+    p.y = static_cast<uint16_t*>(y) + (size_t)r0 * N;
+    if (plan.ksplit > 1) {
+      p.counters = static_cast<uint32_t*>(workspace);
+      p.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    }
+    p.M = rows;
+    p.K = K;
+    p.N = N;
+    p.ksplit = plan.ksplit;
+    p.steps_per_split = plan.steps_per_split;
+    const hipError_t e = mt::launch_dense_qmv(p, dtype, nproj, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, op);
+  }
+  return MT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -223,6 +284,26 @@ int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* bi
       group_size, bits, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "mt_affine_dequantize");
   return MT_OK;
+}
+
+size_t mt_dense_workspace_bytes(int M, int K, int N, int nproj) {
+  if (check_dense("mt_dense_workspace_bytes", M, K, N, MT_BF16)) return 0;
+  return dense_workspace(M, K, N, nproj == 2 ? 2 : 1);
+}
+
+int mt_dense_swiglu(const void* x, const void* gate_w, const void* up_w, void* h, int M, int K,
+                    int N, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  const void* w[2] = {gate_w, up_w};
+  return run_dense("mt_dense_swiglu", 2, x, w, nullptr, h, M, K, N, dtype, workspace,
+                   workspace_bytes, stream);
+}
+
+int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, void* y, int M,
+                          int K, int N, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  const void* ws[2] = {w, nullptr};
+  return run_dense("mt_dense_residual_qmv", 1, x, ws, residual, y, M, K, N, dtype, workspace,
+                   workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,228 @@
+// Dense 16-bit small-batch projections for gfx950: the gate/up SwiGLU and the down projection
+// with a residual epilogue (reference: metile/compiler/dense.py:193-381 with the typed
+// epilogues of metile/codegen/msl_emitter.py:1098-1120,1218-1252).
+//
+// Weights are the native output-major [N, K] matrices. The kernel streams them exactly like
+// the affine kernel (32-column strips, 64-wide K steps split over four waves, a register
+// pipeline of whole K steps, 16-byte buffer loads), but the codes are already 16-bit floats,
+// so each step is four MFMAs chained into the same accumulator and there is no per-step
+// fix-up.
+//
+// Row invariance: the value of every output depends only on its own activation row and on an
+// accumulation order fixed by (K, N): the K partition among splits and waves comes from
+// (K, N) alone, every wave accumulates its steps in order through one MFMA chain, and the
+// cross-wave and split-K sums run in a fixed order. Running a row alone or inside a batch of
+// up to 128 rows therefore gives the same bits. Batches larger than 128 rows run in 128-row
+// chunks.
+#include "common.h"
+#include "dense_qmv.h"
+
+namespace mt {
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+template <int NPROJ, int MT>
+struct DStage {
+  u32x4 w[NPROJ][4];  // 4 x 8 K of column j for each projection
+  u32x4 x[MT][4];     // 4 x 8 K of row j of each 32-row tile
+};
+
+// The reference's typed SwiGLU epilogue: gate and up rounded to the activation type, then
+// y = 1/(1+exp(|g|)), sig = g < 0 ? y : 1 - y, act = g*sig, out = act*u, each operation
+// computed in fp32 and rounded to the activation type.
+template <int DT>
+__device__ __forceinline__ float round_act(float v) {
+  return act_to_f32<DT>(f32_to_act<DT>(v));
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t typed_swiglu(float g, float u) {
+  const float left = round_act<DT>(g);
+  const float right = round_act<DT>(u);
+  const float e = round_act<DT>(expf(fabsf(left)));
+  const float y = round_act<DT>(1.0f / round_act<DT>(1.0f + e));
+  const float sig = left < 0.0f ? y : round_act<DT>(1.0f - y);
+  const float act = round_act<DT>(left * sig);
+  return f32_to_act<DT>(act * right);
+}
+
+template <int DT, int MT, int NPROJ, int STAGES>
+__global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParams p) {
+  __shared__ float red[kWaves][NPROJ][32][33];
+  __shared__ int last_flag;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int strip = blockIdx.x;
+  const int split = blockIdx.y;
+  const int M = p.M, K = p.K, N = p.N;
+  const int steps_total = K >> 6;
+  const int s_beg = split * p.steps_per_split;
+  const int s_end = min(steps_total, s_beg + p.steps_per_split);
+  const int per_wave = (s_end - s_beg + kWaves - 1) / kWaves;
+  const int w_beg = s_beg + wave * per_wave;
+  const int w_end = min(s_end, w_beg + per_wave);
+
+  const uint32_t row_bytes = (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  __amdgpu_buffer_rsrc_t rw[NPROJ];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr) rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * row_bytes);
+  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + 64u * h;
+  uint32_t x_row[MT];
+#pragma unroll
+  for (int rt = 0; rt < MT; ++rt) {
+    const int row = 32 * rt + j;
+    x_row[rt] = row < M ? ((uint32_t)row * K + 32u * h) * 2u : kOOB;
+  }
+
+  DStage<NPROJ, MT> ring[STAGES];
+  auto load_stage = [&](DStage<NPROJ, MT>& S, int st) {
+    const bool ok = st < w_end;
+    const uint32_t woff = w_row + (uint32_t)st * 128u;
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], ok ? woff + 16u * e : kOOB);
+#pragma unroll
+    for (int rt = 0; rt < MT; ++rt) {
+      const bool xok = ok && x_row[rt] != kOOB;
+      const uint32_t xoff = x_row[rt] + (uint32_t)st * 128u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S.x[rt][e] = load16(rx, xok ? xoff + 16u * e : kOOB);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < STAGES; ++d) load_stage(ring[d], w_beg + d);
+
+  f32x16 acc[NPROJ][MT];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int rt = 0; rt < MT; ++rt) acc[pr][rt] = (f32x16){0};
+
+  for (int s0 = w_beg; s0 < w_end; s0 += STAGES) {
+#pragma unroll
+    for (int d = 0; d < STAGES; ++d) {
+      DStage<NPROJ, MT>& S = ring[d];
+      if (s0 + d < w_end) {
+#pragma unroll
+        for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+          for (int rt = 0; rt < MT; ++rt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[pr][rt] = mfma32<DT>(S.x[rt][e], S.w[pr][e], acc[pr][rt]);
+      }
+      load_stage(S, s0 + d + STAGES);
+    }
+  }
+
+  // ---- per row tile: cross-wave reduction (fixed order), then epilogue or split-K -------
+  const size_t plane = (size_t)M * N;
+#pragma unroll
+  for (int rt = 0; rt < MT; ++rt) {
+    if (rt > 0) __syncthreads();
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[wave][pr][mfma32_row(r, h)][j] = acc[pr][rt][r];
+    __syncthreads();
+    const int rows = min(32, M - 32 * rt);
+    for (int o = tid; o < rows * 32; o += kThreads) {
+      const int i = o >> 5, c = o & 31;
+      const size_t oi = (size_t)(32 * rt + i) * N + strip * 32 + c;
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr) {
+        const float v = ((red[0][pr][i][c] + red[1][pr][i][c]) + red[2][pr][i][c]) +
+                        red[3][pr][i][c];
+        if (p.ksplit == 1) {
+          // stash the full sum for the epilogue below
+          red[0][pr][i][c] = v;
+        } else {
+          __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + pr) * plane + oi], v,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      if (p.ksplit == 1) {
+        if constexpr (NPROJ == 2) {
+          p.y[oi] = typed_swiglu<DT>(red[0][0][i][c], red[0][1][i][c]);
+        } else {
+          float out = round_act<DT>(red[0][0][i][c]);
+          if (p.residual) out = out + act_to_f32<DT>(p.residual[oi]);
+          p.y[oi] = f32_to_act<DT>(out);
+        }
+      }
+    }
+  }
+  if (p.ksplit == 1) return;
+
+  // ---- split-K handoff: see the affine kernel; partials and counter are agent-coherent ----
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&p.counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = (prev == (unsigned)(p.ksplit - 1));
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  for (int o = tid; o < M * 32; o += kThreads) {
+    const int i = o >> 5, c = o & 31;
+    const size_t oi = (size_t)i * N + strip * 32 + c;
+    float v[NPROJ];
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr) {
+      float sacc = 0.0f;
+      for (int sp = 0; sp < p.ksplit; ++sp)
+        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + pr) * plane + oi],
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[pr] = sacc;
+    }
+    if constexpr (NPROJ == 2) {
+      p.y[oi] = typed_swiglu<DT>(v[0], v[1]);
+    } else {
+      float out = round_act<DT>(v[0]);
+      if (p.residual) out = out + act_to_f32<DT>(p.residual[oi]);
+      p.y[oi] = f32_to_act<DT>(out);
+    }
+  }
+  if (tid == 0)
+    __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int NPROJ, int MT>
+constexpr int dense_stages() {
+  constexpr int per_stage = 16 * NPROJ + 16 * MT;
+  constexpr int s = 112 / per_stage;
+  return s < 1 ? 1 : s;
+}
+
+template <int DT, int NPROJ>
+hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
+  const dim3 grid(p.N / 32, p.ksplit);
+  if (p.M <= 32) {
+    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>()><<<grid, kThreads, 0, stream>>>(p);
+  } else if (p.M <= 64) {
+    dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>()><<<grid, kThreads, 0, stream>>>(p);
+  } else {
+    dense_qmv_kernel<DT, 4, NPROJ, dense_stages<NPROJ, 4>()><<<grid, kThreads, 0, stream>>>(p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_dense_qmv(const DenseParams& p, int dtype, int nproj, hipStream_t stream) {
+  if (dtype == kBF16)
+    return nproj == 2 ? launch_dense_dt<kBF16, 2>(p, stream) : launch_dense_dt<kBF16, 1>(p, stream);
+  return nproj == 2 ? launch_dense_dt<kF16, 2>(p, stream) : launch_dense_dt<kF16, 1>(p, stream);
+}
+
+}  // namespace mt

@@ -1,0 +1,140 @@
+"""Dense 16-bit small-batch projections on the GPU (Llama-3.2-1B shape,
+hidden 2048, intermediate 8192).
+
+Contract (restating tests/test_mlx_backend.py:274-345): every output row is bit-identical to
+running that row alone, for every M. Parity with the oracle's typed epilogue
+(metile/codegen/msl_emitter.py:1098-1120,1218-1252): at least 99% of outputs bit-exact, and
+every output within 2 ulps of the oracle measured at the magnitude of the epilogue's operands
+(|g*u| for SwiGLU, max(|projection|, |residual|) for the residual add), where each dot
+product's magnitude includes its fp32 accumulation noise, 2^-16 of the sum of absolute
+products. An fp32 accumulation can land on the other side of an intermediate rounding point
+than the fp64 oracle; that moves the typed chain by about one operand ulp, which can be many
+ulps of a near-zero result (a dot product that cancels to 5e-7 from terms of 0.02 carries
+about 1e-7 of fp32 noise).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import metile_amd as mt
+from oracle import affine as O
+from tests.helpers import act_to_torch, torch_to_act
+
+pytestmark = pytest.mark.gpu
+
+H, I = 2048, 8192
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    torch.cuda.set_device(0)
+
+
+def ulp_distance(a, b, dtype="bf16"):
+    """Distance in units in the last place between two arrays of 16-bit patterns."""
+    a = np.asarray(a).view(np.uint16).astype(np.int32)
+    b = np.asarray(b).view(np.uint16).astype(np.int32)
+
+    def ordered(v):
+        return np.where(v & 0x8000, -(v & 0x7FFF), v)
+
+    return np.abs(ordered(a) - ordered(b))
+
+
+def ulp_at(scale, dtype="bf16"):
+    mant = 7 if dtype == "bf16" else 10
+    v = np.maximum(np.abs(np.asarray(scale, dtype=np.float64)), 2.0 ** -120)
+    return np.ldexp(1.0, (np.floor(np.log2(v)) - mant).astype(np.int64))
+
+
+def check_typed(name, got, want, scale, dtype="bf16"):
+    d = ulp_distance(got, want, dtype)
+    exact = float(np.mean(d == 0))
+    diff = np.abs(O.to_f32(got, dtype).astype(np.float64) - O.to_f32(want, dtype))
+    worst = float(np.max(diff / ulp_at(scale, dtype)))
+    print(f"[{name}] exact={exact:.5f} max_ulp={int(d.max())} max_operand_ulps={worst:.2f}",
+          flush=True)
+    assert exact >= 0.99, (name, exact)
+    assert worst <= 2.0, (name, worst)
+
+
+def dots(x, w, dtype="bf16"):
+    """Dot products in float64 widened by their fp32 accumulation noise bound."""
+    xf = O.to_f32(x, dtype).astype(np.float64)
+    wf = O.to_f32(w, dtype).astype(np.float64)
+    return np.abs(xf @ wf.T) + 2.0 ** -16 * (np.abs(xf) @ np.abs(wf).T)
+
+
+@pytest.fixture(scope="module")
+def weights():
+    g = O.make_dense_weight(I, H, 2, 10)
+    u = O.make_dense_weight(I, H, 2, 11)
+    d = O.make_dense_weight(H, I, 2, 12)
+    return {"g": g, "u": u, "d": d,
+            "gt": act_to_torch(g, "bf16"), "ut": act_to_torch(u, "bf16"),
+            "dt": act_to_torch(d, "bf16")}
+
+
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 128])
+def test_dense_swiglu_config2(weights, m):
+    x = O.make_activations(m, H, 2)
+    want = O.dense_swiglu(x, weights["g"], weights["u"])
+    got = mt.mlx_dense_swiglu(act_to_torch(x, "bf16"), mt.DenseWeight.from_torch(weights["gt"]),
+                              mt.DenseWeight.from_torch(weights["ut"]))
+    scale = dots(x, weights["g"]) * dots(x, weights["u"])
+    check_typed(f"dense swiglu M={m}", torch_to_act(got, "bf16"), want, scale)
+
+
+@pytest.mark.parametrize("m", [1, 7, 32, 128])
+def test_dense_residual_config2(weights, m):
+    h = O.make_activations(m, I, 2, tensor_id=5)
+    r = O.make_activations(m, H, 2, tensor_id=3)
+    want = O.dense_residual_qmv(h, weights["d"], r)
+    got = mt.mlx_dense_residual_qmv(act_to_torch(h, "bf16"), weights["dt"],
+                                    act_to_torch(r, "bf16"))
+    scale = np.maximum(np.abs(dots(h, weights["d"])), np.abs(O.to_f32(r, "bf16")))
+    check_typed(f"dense residual M={m}", torch_to_act(got, "bf16"), want, scale)
+
+
+def test_dense_projection_without_residual_and_f16():
+    k, n, m = 512, 96, 5
+    x = O.make_activations(m, k, 21, dtype="f16")
+    w = O.make_dense_weight(n, k, 21, 10, dtype="f16")
+    want = O.dense_residual_qmv(x, w, None, dtype="f16")
+    got = mt.dense_qmv(act_to_torch(x, "f16"), act_to_torch(w, "f16"))
+    check_typed("dense f16 no residual", torch_to_act(got, "f16"), want, dots(x, w, "f16"), "f16")
+
+
+@pytest.mark.parametrize("m", [2, 5, 16, 33, 64, 128, 130])
+def test_dense_rows_bit_identical_to_single_row_runs(weights, m):
+    x = act_to_torch(O.make_activations(m, H, 3), "bf16")
+    r = act_to_torch(O.make_activations(m, H, 3, tensor_id=3), "bf16")
+    g = mt.DenseWeight.from_torch(weights["gt"])
+    u = mt.DenseWeight.from_torch(weights["ut"])
+    batch_h = mt.mlx_dense_swiglu(x, g, u)
+    batch_y = mt.mlx_dense_residual_qmv(batch_h, weights["dt"], r)
+    rows = range(m) if m <= 16 else sorted({0, 1, m // 2, m - 2, m - 1, 31 % m, 32 % m})
+    for row in rows:
+        one_h = mt.mlx_dense_swiglu(x[row:row + 1], g, u)
+        one_y = mt.mlx_dense_residual_qmv(one_h, weights["dt"], r[row:row + 1])
+        assert torch.equal(one_h.view(torch.int16), batch_h[row:row + 1].view(torch.int16)), \
+            (m, row, "swiglu")
+        assert torch.equal(one_y.view(torch.int16), batch_y[row:row + 1].view(torch.int16)), \
+            (m, row, "residual")
+
+
+def test_dense_leading_dims_and_empty(weights):
+    x = act_to_torch(O.make_activations(6, H, 4), "bf16")
+    g = mt.DenseWeight.from_torch(weights["gt"])
+    u = mt.DenseWeight.from_torch(weights["ut"])
+    flat = mt.mlx_dense_swiglu(x, g, u)
+    shaped = mt.mlx_dense_swiglu(x.reshape(2, 3, H), g, u)
+    assert tuple(shaped.shape) == (2, 3, I)
+    assert torch.equal(shaped.reshape(6, I).view(torch.int16), flat.view(torch.int16))
+    empty = mt.dense_swiglu(x[:0], weights["gt"], weights["ut"])
+    assert tuple(empty.shape) == (0, I)

@@ -84,3 +84,44 @@ def test_operators_reject_host_tensors():
     w, s, b = _affine(64, 128)
     with pytest.raises(ValueError, match="ROCm device tensors"):
         mt.affine_qmv(x, w, s, b)
+
+
+# ---- dense (metile/backends/mlx_dense_swiglu.py:424-447, mlx_dense_residual.py:276-288) ----
+
+
+def test_dense_weight_validation():
+    with pytest.raises(ValueError, match="shape \\[output, input\\]"):
+        mt.DenseWeight.from_torch(torch.zeros(4, dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="bfloat16 or float16"):
+        mt.DenseWeight.from_torch(torch.zeros(4, 4, dtype=torch.float32))
+    assert mt.DenseWeight.from_torch(torch.zeros(64, 128, dtype=torch.bfloat16)).shape == (128, 64)
+
+
+def test_dense_swiglu_guards():
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    g = mt.DenseWeight.from_torch(torch.zeros(64, 128, dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="must be DenseWeight"):
+        mt.mlx_dense_swiglu(x, g.native_weight, g)
+    u2 = mt.DenseWeight.from_torch(torch.zeros(32, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="matching shapes"):
+        mt.mlx_dense_swiglu(x, g, u2)
+    with pytest.raises(ValueError, match="values\\[..., K\\]"):
+        mt.mlx_dense_swiglu(torch.zeros(2, 64, dtype=torch.bfloat16), g, g)
+    with pytest.raises(TypeError, match="matching activation and weight dtypes"):
+        mt.mlx_dense_swiglu(x.half(), g, g)
+    with pytest.raises(ValueError, match="paired dense SwiGLU weight"):
+        mt.mlx_dense_swiglu(x, g, g, paired_weight=torch.zeros(64, 128, dtype=torch.bfloat16))
+
+
+def test_dense_residual_guards():
+    x = torch.zeros(2, 128, dtype=torch.bfloat16)
+    w = torch.zeros(64, 128, dtype=torch.bfloat16)
+    r = torch.zeros(2, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="rank-compatible"):
+        mt.mlx_dense_residual_qmv(x, w, r[0])
+    with pytest.raises(ValueError, match="input features must match"):
+        mt.mlx_dense_residual_qmv(x, w[:, :64], r)
+    with pytest.raises(ValueError, match="residual shape"):
+        mt.mlx_dense_residual_qmv(x, w, torch.zeros(2, 32, dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="matching input dtypes"):
+        mt.mlx_dense_residual_qmv(x, w.half(), r)
