@@ -86,6 +86,20 @@ int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* bi
                          float* out, int N, int K, int group_size, int bits, int dtype,
                          void* stream);
 
+/* ---- prefill (many rows) ---------------------------------------------------------------- */
+
+/* Workspace bytes mt_affine_gemm needs (0 when K is not split). */
+size_t mt_affine_gemm_workspace_bytes(int M, int K, int N, int group_size, int bits);
+
+/* y = x @ dequantize(w_q)^T for many rows (prefill): the codes are dequantized to the
+ * activation type (q*s + b in fp32, then rounded) in LDS and multiplied on the matrix cores
+ * with fp32 accumulation. Replaces mlx_affine_matmul / lower_affine_matmul
+ * (metile/backends/mlx_affine.py:359-406, metile/compiler/affine_quantized.py:7-99).
+ * bits = 4; group_size a power of two >= 64 dividing K; K % 64 == 0; N % 32 == 0. */
+int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
+                   void* y, int M, int K, int N, int group_size, int bits, int dtype,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- dense 16-bit small-batch projections ------------------------------------------------ */
 
 /* Workspace bytes mt_dense_swiglu (nproj = 2) or mt_dense_residual_qmv (nproj = 1) needs. */

@@ -8,10 +8,13 @@ reference's call surface (``metile/backends/mlx_quantized.py``).
 from ._lib import MetileError, version
 from .dense import DenseWeight, dense_qmv, dense_swiglu, mlx_dense_residual_qmv, mlx_dense_swiglu
 from .quantized import (
+    AffineWeight,
     affine_dequantize,
+    affine_matmul,
     affine_mlp,
     affine_qmv,
     affine_swiglu,
+    mlx_affine_matmul,
     mlx_affine_mlp_executor,
     mlx_affine_qmv,
     mlx_affine_residual_qmv,
@@ -21,6 +24,7 @@ from .quantized import (
 )
 
 __all__ = [
+    "AffineWeight",
     "DenseWeight",
     "MetileError",
     "dense_qmv",
@@ -28,9 +32,11 @@ __all__ = [
     "mlx_dense_residual_qmv",
     "mlx_dense_swiglu",
     "affine_dequantize",
+    "affine_matmul",
     "affine_mlp",
     "affine_qmv",
     "affine_swiglu",
+    "mlx_affine_matmul",
     "mlx_affine_mlp_executor",
     "mlx_affine_qmv",
     "mlx_affine_residual_qmv",

@@ -1,0 +1,246 @@
+// Prefill affine quantized GEMM for gfx950: y[M, N] = x[M, K] @ dequantize(w_q)[N, K]^T for
+// many rows (reference: lower_affine_matmul, metile/compiler/affine_quantized.py:7-99, and its
+// dispatcher mlx_affine_matmul, metile/backends/mlx_affine.py:359-406).
+//
+// Design: a workgroup computes a BM x BN output tile with a 2 x 2 grid of waves, each wave
+// TM x TN tiles of MFMA 32x32x16 (fp32 accumulate). The K loop runs in 64-wide steps through a
+// double-buffered LDS pipeline: the next step's activation tile and packed codes are loaded
+// into registers while the current step's MFMAs run from LDS, then the codes are turned into
+// exact 16-bit floats (offset + q) and written to the other LDS buffer with the activation
+// tile, the per-row sums of the activation tile and the per-column scale and bias.
+// Dequantization stays exact: each step's MFMA partial t = sum_k x_k (offset + q_k) gets its
+// group's affine terms in fp32, acc += s * t + (b - offset * s) * sum_k x_k, exactly as in the
+// small-row kernel. Rows beyond M and columns beyond N read zero through the buffer range
+// check and are not stored.
+#include "common.h"
+#include "affine_gemm.h"
+
+namespace mt {
+
+namespace {
+
+constexpr int kBK = 64;        // K per pipeline step
+constexpr int kPad = 8;        // LDS row padding, in 16-bit elements
+constexpr int kLdsRow = kBK + kPad;
+
+template <int DT, int TM, int TN>
+__global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p) {
+  constexpr int BM = 64 * TM;
+  constexpr int BN = 64 * TN;
+  constexpr int kAChunks = BM * kBK * 2 / 16 / 256;  // 16-byte activation chunks per thread
+  constexpr float kOff = CodeOffset<4, DT>::value;
+  static_assert(kAChunks >= 1, "tile too small");
+
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kLdsRow];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][kLdsRow];
+  __shared__ __attribute__((aligned(16))) float Xs[2][BM];   // per-row sums of the step
+  __shared__ float Ss[2][BN], Bp[2][BN];                     // scale, bias - offset*scale
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int j = lane & 31, h = lane >> 5;
+  const int M = p.M, K = p.K, N = p.N;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int steps = K / kBK;
+  const int s_beg = blockIdx.z * p.steps_per_split;
+  const int s_end = min(steps, s_beg + p.steps_per_split);
+
+  const uint32_t row_bytes = (uint32_t)K / 2u;
+  const int groups_per_row = K / p.G;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, (uint32_t)N * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s, (uint32_t)N * groups_per_row * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b, (uint32_t)N * groups_per_row * 2u);
+
+  // Activation tile: chunk c = tid + 256 i covers row c / 8, 16 bytes (c % 8) of the step.
+  uint32_t a_off[kAChunks];
+  int a_row[kAChunks], a_col[kAChunks];
+#pragma unroll
+  for (int i = 0; i < kAChunks; ++i) {
+    const int c = tid + 256 * i;
+    a_row[i] = c >> 3;
+    a_col[i] = (c & 7) * 8;
+    const int gr = m0 + a_row[i];
+    a_off[i] = gr < M ? ((uint32_t)gr * K + a_col[i]) * 2u : kOOB;
+  }
+  // Codes: thread t < 2*BN loads K half (t & 1) of column t >> 1 (16 bytes = 32 codes).
+  const bool b_active = tid < 2 * BN;
+  const int b_col = tid >> 1, b_half = tid & 1;
+  const int gcol = n0 + b_col;
+  const bool col_ok = b_active && gcol < N;
+  const uint32_t b_off = col_ok ? (uint32_t)gcol * row_bytes + 16u * b_half : kOOB;
+  const uint32_t g_off = col_ok ? (uint32_t)gcol * groups_per_row * 2u : kOOB;
+  // Row sums: thread t < 2*BM sums half (t & 1) of row t >> 1 of the activation tile.
+  const bool x_active = tid < 2 * BM;
+  const int x_row = tid >> 1, x_half = tid & 1;
+
+  u32x4 ra[kAChunks];
+  u32x4 rc;
+  uint32_t rsv, rbv;
+  auto load_step = [&](int st) {
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i)
+      ra[i] = load16(rx, a_off[i] == kOOB ? kOOB : a_off[i] + (uint32_t)st * 128u);
+    rc = load16(rw, b_off == kOOB ? kOOB : b_off + (uint32_t)st * 32u);
+    const uint32_t go = g_off == kOOB ? kOOB : g_off + (uint32_t)((st * kBK) / p.G) * 2u;
+    rsv = load2(rs, go);
+    rbv = load2(rb, go);
+  };
+  auto store_step = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < kAChunks; ++i)
+      *reinterpret_cast<u32x4*>(&As[buf][a_row[i]][a_col[i]]) = ra[i];
+    if (b_active) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<u32x4*>(&Bs[buf][b_col][32 * b_half + 8 * q]) = unpack_u4<DT>(rc[q]);
+      if (b_half == 0) {
+        const float sf = act_to_f32<DT>(rsv);
+        Ss[buf][b_col] = sf;
+        Bp[buf][b_col] = __builtin_fmaf(-kOff, sf, act_to_f32<DT>(rbv));
+      }
+    }
+  };
+  // Per-row sums of a stored activation tile (call after the barrier that publishes it).
+  auto sum_rows = [&](int buf) {
+    float acc = 0.0f;
+    if (x_active) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        acc = sum8<DT>(*reinterpret_cast<const u32x4*>(&As[buf][x_row][32 * x_half + 8 * q]), acc);
+    }
+    acc += __shfl_xor(acc, 1);
+    if (x_active && x_half == 0) Xs[buf][x_row] = acc;
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b) acc[a][b] = (f32x16){0};
+
+  if (s_beg < s_end) {
+    load_step(s_beg);
+    store_step(0);
+  }
+  __syncthreads();
+  if (s_beg < s_end) sum_rows(0);
+  __syncthreads();
+  const f32x16 zero16 = (f32x16){0};
+  for (int st = s_beg; st < s_end; ++st) {
+    const int buf = (st - s_beg) & 1;
+    const bool more = st + 1 < s_end;
+    if (more) load_step(st + 1);
+    f32x16 t[TM][TN];
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      u32x4 af[TM], bfr[TN];
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+        af[a] = *reinterpret_cast<const u32x4*>(
+            &As[buf][wm * 32 * TM + 32 * a + j][16 * kk + 8 * h]);
+#pragma unroll
+      for (int b = 0; b < TN; ++b)
+        bfr[b] = *reinterpret_cast<const u32x4*>(
+            &Bs[buf][wn * 32 * TN + 32 * b + j][16 * kk + 8 * h]);
+#pragma unroll
+      for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < TN; ++b)
+          t[a][b] = mfma32<DT>(af[a], bfr[b], kk == 0 ? zero16 : t[a][b]);
+    }
+    // Affine terms of the step's group, per column (lane) and row (register).
+#pragma unroll
+    for (int b = 0; b < TN; ++b) {
+      const int col = wn * 32 * TN + 32 * b + j;
+      const float sf = Ss[buf][col];
+      const float bp = Bp[buf][col];
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const f32x4 xs = *reinterpret_cast<const f32x4*>(
+              &Xs[buf][wm * 32 * TM + 32 * a + 8 * r4 + 4 * h]);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int r = 4 * r4 + v;
+            acc[a][b][r] = __builtin_fmaf(sf, t[a][b][r], acc[a][b][r]);
+            acc[a][b][r] = __builtin_fmaf(bp, xs[v], acc[a][b][r]);
+          }
+        }
+      }
+    }
+    if (more) store_step(buf ^ 1);
+    __syncthreads();
+    if (more) sum_rows(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: fp32 tile -> activation type (or split-K fp32 partials) -----------------
+#pragma unroll
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TN; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 32 * TM + 32 * a + mfma32_row(r, h);
+        const int col = n0 + wn * 32 * TN + 32 * b + j;
+        if (row < M && col < N) {
+          if (p.ksplit == 1) {
+            p.y[(size_t)row * N + col] = f32_to_act<DT>(acc[a][b][r]);
+          } else {
+            __hip_atomic_store(&p.partial[((size_t)blockIdx.z * M + row) * N + col],
+                               acc[a][b][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+  if (p.ksplit == 1) return;
+
+  // Split-K: the last workgroup of an output tile sums the partials in split order.
+  __shared__ int last_flag;
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = (prev == (unsigned)(p.ksplit - 1));
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  for (int o = tid; o < BM * BN; o += 256) {
+    const int row = m0 + o / BN, col = n0 + o % BN;
+    if (row >= M || col >= N) continue;
+    float v = 0.0f;
+    for (int sp = 0; sp < p.ksplit; ++sp)
+      v += __hip_atomic_load(&p.partial[((size_t)sp * M + row) * N + col], __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    p.y[(size_t)row * N + col] = f32_to_act<DT>(v);
+  }
+  if (tid == 0)
+    __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int TM, int TN>
+hipError_t launch_tile(const GemmParams& p, hipStream_t stream) {
+  const dim3 grid((p.N + 64 * TN - 1) / (64 * TN), (p.M + 64 * TM - 1) / (64 * TM), p.ksplit);
+  affine_gemm_kernel<DT, TM, TN><<<grid, 256, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_dt(const GemmParams& p, hipStream_t stream) {
+  if (p.tile == 2) return launch_tile<DT, 2, 2>(p, stream);
+  return launch_tile<DT, 1, 1>(p, stream);
+}
+
+}  // namespace
+
+hipError_t launch_affine_gemm(const GemmParams& p, int dtype, hipStream_t stream) {
+  return dtype == kBF16 ? launch_dt<kBF16>(p, stream) : launch_dt<kF16>(p, stream);
+}
+
+}  // namespace mt

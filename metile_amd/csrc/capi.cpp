@@ -10,6 +10,7 @@
 
 #include "affine_qmv.h"
 #include "dense_qmv.h"
+#include "affine_gemm.h"
 
 namespace {
 
@@ -197,6 +198,45 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
   return MT_OK;
 }
 
+// Prefill GEMM plan: 128 x 128 tiles when they give at least about one workgroup per CU,
+// else 64 x 64 tiles; K is split when the tiles alone leave the chip underused.
+struct GemmPlan {
+  int tile;
+  int tiles;
+  int ksplit;
+  int steps_per_split;
+};
+
+GemmPlan plan_gemm(int M, int K, int N) {
+  GemmPlan g;
+  const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
+  const int t64 = ((M + 63) / 64) * ((N + 63) / 64);
+  g.tile = t128 >= 200 ? 2 : 1;
+  if (const char* env = std::getenv("METILE_AMD_GEMM_TILE")) g.tile = std::atoi(env) == 2 ? 2 : 1;
+  g.tiles = g.tile == 2 ? t128 : t64;
+  // About three workgroups per CU in total, keeping at least 24 K steps per split (measured
+  // on MI355X at Qwen2.5-1.5B prefill shapes: up 1536x8960 best unsplit, down 8960x1536 best
+  // with four splits of 64 x 64 tiles).
+  const int steps = K / 64;
+  int ksplit = (768 + g.tiles / 2) / g.tiles;
+  const int max_split = steps / 24 > 0 ? steps / 24 : 1;
+  if (ksplit > max_split) ksplit = max_split;
+  if (ksplit < 1) ksplit = 1;
+  if (const char* env = std::getenv("METILE_AMD_GEMM_KSPLIT")) {
+    const int f = std::atoi(env);
+    if (f >= 1 && f <= steps) ksplit = f;
+  }
+  g.steps_per_split = (steps + ksplit - 1) / ksplit;
+  g.ksplit = (steps + g.steps_per_split - 1) / g.steps_per_split;
+  return g;
+}
+
+size_t gemm_workspace(int M, int K, int N) {
+  const GemmPlan g = plan_gemm(M, K, N);
+  if (g.ksplit <= 1) return 0;
+  return kCounterBytes + (size_t)g.ksplit * M * N * 4;
+}
+
 }  // namespace
 
 extern "C" {
@@ -304,6 +344,54 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
   const void* ws[2] = {w, nullptr};
   return run_dense("mt_dense_residual_qmv", 1, x, ws, residual, y, M, K, N, dtype, workspace,
                    workspace_bytes, stream);
+}
+
+size_t mt_affine_gemm_workspace_bytes(int M, int K, int N, int group_size, int bits) {
+  if (check_affine("mt_affine_gemm_workspace_bytes", 1, K, N, group_size, bits, MT_BF16) ||
+      M < 1)
+    return 0;
+  return gemm_workspace(M, K, N);
+}
+
+int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
+                   void* y, int M, int K, int N, int group_size, int bits, int dtype,
+                   void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_affine("mt_affine_gemm", 1, K, N, group_size, bits, dtype);
+  if (st) return st;
+  if (bits != 4)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: the prefill GEMM takes 4-bit codes");
+  if (M < 1) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: M must be positive");
+  if ((size_t)M * K * 2 >= (1ull << 31) || (size_t)M * N >= (1ull << 31))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: tensor larger than 2 GiB");
+  if (!x || !w_q || !scales || !biases || !y)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: null pointer");
+  const GemmPlan g = plan_gemm(M, K, N);
+  const size_t need = gemm_workspace(M, K, N);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(MT_ERR_WORKSPACE, "mt_affine_gemm: workspace of " + std::to_string(need) +
+                                      " bytes required, got " + std::to_string(workspace_bytes));
+  if (g.ksplit > 1 && g.tiles > kMaxStrips)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: too many output tiles to split K");
+  mt::GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.w = w_q;
+  p.s = static_cast<const uint16_t*>(scales);
+  p.b = static_cast<const uint16_t*>(biases);
+  p.y = static_cast<uint16_t*>(y);
+  if (g.ksplit > 1) {
+    p.counters = static_cast<uint32_t*>(workspace);
+    p.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+  }
+  p.M = M;
+  p.K = K;
+  p.N = N;
+  p.G = group_size;
+  p.tile = g.tile;
+  p.ksplit = g.ksplit;
+  p.steps_per_split = g.steps_per_split;
+  const hipError_t e = mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_affine_gemm");
+  return MT_OK;
 }
 
 }  // extern "C"

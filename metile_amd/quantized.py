@@ -15,6 +15,7 @@ Tensor formats (MLX affine): ``weight`` uint32 (or int32 holding the same bits)
 from __future__ import annotations
 
 import threading
+from dataclasses import dataclass
 
 import torch
 
@@ -223,6 +224,65 @@ def affine_dequantize(weight, scales, biases, *, group_size=64, bits=4):
     return out
 
 
+def affine_matmul(values, weight, scales, biases, *, group_size=64, bits=4):
+    """Prefill ``values @ dequantize(weight).T`` for many rows: codes are dequantized to the
+    activation type in LDS and multiplied on the matrix cores (fp32 accumulation), the
+    semantics of MLX's quantized matmul for large row counts
+    (``metile/backends/mlx_affine.py:142-154``)."""
+    if biases is None:
+        raise ValueError("affine matmul requires affine quantization biases")
+    _require_device(values, weight, scales, biases)
+    code = _dtype_code(values.dtype)
+    _check_params(values, weight, scales, biases, group_size, bits, "affine matmul")
+    k = values.shape[-1]
+    n = weight.shape[0]
+    lead = tuple(values.shape[:-1])
+    x = values.reshape(-1, k).contiguous()
+    m = x.shape[0]
+    out = torch.empty(*lead, n, dtype=values.dtype, device=values.device)
+    if m == 0:
+        return out
+    w = _as_u32(weight)
+    s, b = scales.contiguous(), biases.contiguous()
+    lib = _lib.lib()
+    need = lib.mt_affine_gemm_workspace_bytes(m, k, n, group_size, bits)
+    ws = workspace(values.device, need) if need else None
+    _lib.check(lib.mt_affine_gemm(
+        x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), out.data_ptr(), m, k, n,
+        group_size, bits, code, _ptr(ws), 0 if ws is None else ws.numel(),
+        _stream_handle(values.device)))
+    return out
+
+
+@dataclass(frozen=True)
+class AffineWeight:
+    """One affine 4-bit weight for the prefill path, ``shape = (K, N)``.
+
+    Counterpart of ``MLXAffineWeight`` (``metile/backends/mlx_affine.py:66-114``). The gfx950
+    GEMM reads the native MLX output-major words directly, so no K-major repack is kept.
+    """
+
+    native_weight: torch.Tensor
+    native_scales: torch.Tensor
+    native_biases: torch.Tensor
+    shape: tuple
+    group_size: int = 64
+    bits: int = 4
+
+    @classmethod
+    def from_torch(cls, weight, scales, biases, *, group_size=64, bits=4):
+        if group_size != 64 or bits != 4:
+            raise ValueError(
+                f"affine prefill weights require group size 64 and 4 bits, got {group_size} and "
+                f"{bits}")
+        if biases is None:
+            raise ValueError("native affine QMV requires affine biases")
+        if weight.ndim != 2 or scales.ndim != 2 or biases.shape != scales.shape:
+            raise ValueError("expected packed weight and matching two-dimensional parameters")
+        k = weight.shape[1] * 32 // bits
+        return cls(weight, scales, biases, (k, weight.shape[0]), group_size, bits)
+
+
 # ---------------------------------------------------------------------------------------------
 # reference-named entry points (metile/backends/mlx_quantized.py)
 # ---------------------------------------------------------------------------------------------
@@ -343,3 +403,17 @@ def mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual, *, 
         raise ValueError("affine residual QMV parameters must match the input dtype")
     if tuple(residual.shape) != (*values.shape[:-1], n) or residual.dtype != values.dtype:
         raise ValueError("residual must match the affine QMV output shape and dtype")
+
+
+def mlx_affine_matmul(values, weight, *, autotune=True):
+    """Drop-in for ``mlx_affine_matmul`` (``metile/backends/mlx_affine.py:359-406``) with the
+    reference's guards. The reference's Metal path takes float16 only; the gfx950 GEMM also
+    takes bfloat16 (BASELINE config 4 is bf16), and any other dtype raises ``TypeError``."""
+    if not isinstance(weight, AffineWeight):
+        raise TypeError("weight must be an AffineWeight")
+    if values.ndim < 2 or values.shape[-1] != weight.shape[0]:
+        raise ValueError("expected values[..., K] and a KxN affine weight")
+    if values.dtype not in _DTYPES:
+        raise TypeError("affine matmul requires float16 or bfloat16 activations")
+    return affine_matmul(values, weight.native_weight, weight.native_scales,
+                         weight.native_biases, group_size=weight.group_size, bits=weight.bits)

@@ -125,3 +125,25 @@ def test_dense_residual_guards():
         mt.mlx_dense_residual_qmv(x, w, torch.zeros(2, 32, dtype=torch.bfloat16))
     with pytest.raises(TypeError, match="matching input dtypes"):
         mt.mlx_dense_residual_qmv(x, w.half(), r)
+
+
+# ---- prefill (metile/backends/mlx_affine.py:80-114,359-366) -------------------------------
+
+
+def test_affine_weight_requires_4bit_group64():
+    w, s, b = _affine(64, 128, bits=8)
+    with pytest.raises(ValueError, match="group size 64 and 4 bits"):
+        mt.AffineWeight.from_torch(w, s, b, bits=8)
+    w, s, b = _affine(64, 128)
+    assert mt.AffineWeight.from_torch(w, s, b).shape == (128, 64)
+
+
+def test_affine_matmul_guards():
+    w, s, b = _affine(64, 128)
+    aw = mt.AffineWeight.from_torch(w, s, b)
+    with pytest.raises(TypeError, match="AffineWeight"):
+        mt.mlx_affine_matmul(torch.zeros(2, 128, dtype=torch.bfloat16), w)
+    with pytest.raises(ValueError, match="values\\[..., K\\]"):
+        mt.mlx_affine_matmul(torch.zeros(2, 64, dtype=torch.bfloat16), aw)
+    with pytest.raises(TypeError, match="float16 or bfloat16"):
+        mt.mlx_affine_matmul(torch.zeros(2, 128, dtype=torch.float32), aw)
