@@ -1,19 +1,26 @@
-"""Benchmark of the INT4 affine quantized MLP hot path on one MI355X.
+"""Benchmark of the quantized-projection hot path on one MI355X.
 
-Workload: the INT4 fused SwiGLU MLP at Qwen2.5-1.5B shape (hidden 1536,
-intermediate 8960, group 64, bf16 activations) over a stack of 28 distinct layers (650 MB of
-packed weights, 2.5x the 256 MB Infinity Cache), so every step streams its weights from HBM.
-A step is one pass of the hot path over one batch: the M=1 decode row through all 28 layer
-MLPs (gate/up SwiGLU kernel, then the down projection with the residual epilogue), replayed
-from a HIP graph. Weights are seeded synthetic data of the BASELINE recipe (codes uniform in
-0..15, scale = |N(0,1)|*0.02 in bf16, bias = -8*scale).
+Headline workload: the INT4 fused SwiGLU MLP at Qwen2.5-1.5B shape (hidden
+1536, intermediate 8960, group 64, bf16 activations) over a stack of 28 distinct layers
+(650 MB of packed weights, 2.5x the 256 MB Infinity Cache), so every step streams its weights
+from HBM. A step is one pass of the hot path over one batch: the M=1 decode row through all 28
+layer MLPs (fused gate/up SwiGLU kernel, then the down projection with the residual epilogue),
+replayed from a HIP graph whose outputs are first checked bit-for-bit against an eager run.
+Weights are seeded synthetic data of the BASELINE recipe (codes uniform in 0..15,
+scale = |N(0,1)|*0.02 in bf16, bias = -8*scale).
 
-``value`` is the whole-job algorithmic HBM throughput of the M=1 step (packed weights,
-scales, biases, activations in and out). The JSON line also carries the per-row sweep
-(M = 1..32), the roofline of the dominant kernel (the fused SwiGLU kernel, timed with HIP
-events on the stream it runs on) and the CPU baseline (the NumPy oracle on this host).
+``value`` is the whole-job algorithmic HBM throughput of the M=1 step: packed weights, scales,
+biases, activations in and out. The JSON line also carries:
+* ``rows``: the same MLP at M = 1, 2, 4, 8, 16, 32 (us per layer call, GB/s);
+* ``roofline``: the dominant kernel (the fused SwiGLU at M=1), timed alone with HIP events on
+  the stream it runs on;
+* ``configs``: the other BASELINE configs (0: one INT4 projection 1536->8960 at M=1..32;
+  2: dense BF16 MLP at Llama-3.2-1B shape; 3: INT8 projection 5120->17408; 4: INT4 prefill
+  GEMM at M=512), each over enough distinct weight copies to defeat the Infinity Cache;
+* ``ceiling``: the measured streaming-read rate of one launch at the same byte counts;
+* ``cpu_baseline``: the NumPy oracle on this host's cores.
 
-Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W]``.
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]``.
 """
 
 from __future__ import annotations
@@ -29,29 +36,34 @@ import torch
 HIDDEN, INTER, GROUP, BITS, LAYERS = 1536, 8960, 64, 4, 28
 ROWS = (1, 2, 4, 8, 16, 32)
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+STACK_BYTES = 600 << 20  # distinct weight bytes per timed rotation (> 2x the 256 MB MALL)
 
 
-def proj_weight_bytes(k, n):
-    return n * k * BITS // 8 + 2 * 2 * n * (k // GROUP)
+def proj_weight_bytes(k, n, bits=BITS, group=GROUP):
+    return n * k * bits // 8 + 2 * 2 * n * (k // group)
 
 
 def mlp_bytes(m):
     """Algorithmic bytes of one layer MLP call at m rows: gate+up+down packed weights, scales
-    and biases, x in, residual in, y out (the hidden activation round trip is counted too)."""
+    and biases, x in, residual in, y out, and the hidden activation's store and reload."""
     w = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
     act = 2 * m * HIDDEN * 3 + 2 * 2 * m * INTER
     return w + act
 
 
+def make_affine(gen, device, k, n, bits=BITS, group=GROUP):
+    words = torch.randint(-2**31, 2**31, (n, k * bits // 32), generator=gen, device=device,
+                          dtype=torch.int64).to(torch.int32)
+    coef, zero = (0.02, 8.0) if bits == 4 else (0.002, 128.0)
+    s = (torch.randn(n, k // group, generator=gen, device=device).abs() * coef).to(torch.bfloat16)
+    b = (s.float() * -zero).to(torch.bfloat16)
+    return words, s, b
+
+
 def make_layer(gen, device):
-    def proj(k, n):
-        words = torch.randint(-2**31, 2**31, (n, k * BITS // 32), generator=gen, device=device,
-                              dtype=torch.int64).to(torch.int32)
-        s = (torch.randn(n, k // GROUP, generator=gen, device=device).abs() * 0.02)
-        s = s.to(torch.bfloat16)
-        b = (s.float() * -8.0).to(torch.bfloat16)
-        return words, s, b
-    return proj(HIDDEN, INTER), proj(HIDDEN, INTER), proj(INTER, HIDDEN)
+    return (make_affine(gen, device, HIDDEN, INTER), make_affine(gen, device, HIDDEN, INTER),
+            make_affine(gen, device, INTER, HIDDEN))
 
 
 def time_graph(graph, stream, steps, warmup):
@@ -73,6 +85,168 @@ def capture(fn, stream):
     with torch.cuda.graph(g, stream=stream):
         fn()
     return g
+
+
+def timed(fn, stream, steps, warmup, calls):
+    """Run ``fn`` eagerly (allocates workspaces outside capture), capture it, check that a
+    replay reproduces the eager outputs bit for bit, and return us per call."""
+    outs = fn()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    holder = {}
+
+    def body():
+        holder["outs"] = fn()
+
+    graph = capture(body, stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    for a, b in zip(eager, holder["outs"]):
+        if not torch.equal(a.view(torch.int16), b.view(torch.int16)):
+            raise RuntimeError("graph replay differs from the eager run")
+    return time_graph(graph, stream, steps, warmup) * 1e3 / calls
+
+
+def copies_for(nbytes):
+    return max(2, -(-STACK_BYTES // nbytes))
+
+
+# ---- sections ---------------------------------------------------------------------------------
+
+
+def section_mlp(mt, gen, device, stream, args):
+    layers = [make_layer(gen, device) for _ in range(LAYERS)]
+    wbytes = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
+    rows_out, kernel, step_ms = {}, {}, None
+    for m in ROWS:
+        x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+        res = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+
+        def stack():
+            return [mt.affine_mlp(x, g, u, d, group_size=GROUP, bits=BITS, residual=res)
+                    for (g, u, d) in layers]
+
+        steps = args.steps if m == 1 else max(10, args.steps // 4)
+        us = timed(stack, stream, steps, args.warmup, LAYERS)
+        rows_out[str(m)] = {
+            "us_per_mlp_call": round(us, 3),
+            "hbm_GBps": round(mlp_bytes(m) / us / 1e3, 1),
+            "weight_GBps": round(wbytes / us / 1e3, 1),
+            "frac_of_peak": round(mlp_bytes(m) / us / 1e3 / HBM_PEAK_GBS, 4),
+        }
+        if m == 1:
+            step_ms = us * LAYERS / 1e3
+            hs = [torch.randn(m, INTER, generator=gen, device=device).to(torch.bfloat16)
+                  for _ in range(LAYERS)]
+
+            def swiglu():
+                return [mt.affine_swiglu(x, *g, *u, group_size=GROUP, bits=BITS)
+                        for (g, u, _d) in layers]
+
+            def down():
+                return [mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
+                        for h, (_g, _u, d) in zip(hs, layers)]
+
+            kernel["swiglu_us"] = timed(swiglu, stream, args.steps, args.warmup, LAYERS)
+            kernel["down_us"] = timed(down, stream, args.steps, args.warmup, LAYERS)
+            kernel["swiglu_bytes"] = (2 * proj_weight_bytes(HIDDEN, INTER) + 2 * m * HIDDEN
+                                      + 2 * m * INTER)
+            kernel["down_bytes"] = proj_weight_bytes(INTER, HIDDEN) + 2 * m * INTER + 4 * m * HIDDEN
+    del layers
+    return rows_out, kernel, step_ms
+
+
+def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
+    """One affine projection over a rotation of distinct copies (configs 0 and 3)."""
+    wb = proj_weight_bytes(k, n, bits)
+    copies = copies_for(wb)
+    ws = [make_affine(gen, device, k, n, bits) for _ in range(copies)]
+    out = {}
+    for m in rows:
+        x = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
+        us = timed(lambda: [mt.affine_qmv(x, *w, group_size=GROUP, bits=bits) for w in ws],
+                   stream, max(10, args.steps // 4), args.warmup, copies)
+        total = wb + 2 * m * k + 2 * m * n
+        out[str(m)] = {"us": round(us, 3), "hbm_GBps": round(total / us / 1e3, 1),
+                       "frac_of_peak": round(total / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del ws
+    return {"K": k, "N": n, "bits": bits, "group_size": GROUP, "copies": copies,
+            "bytes_per_call_M1": wb + 2 * k + 2 * n, "rows": out}
+
+
+def section_dense(mt, gen, device, stream, args):
+    """Dense BF16 SwiGLU MLP at Llama-3.2-1B shape (config 2)."""
+    h, i = 2048, 8192
+    wbytes = 3 * 2 * h * i
+    copies = copies_for(wbytes)
+    ws = [tuple((torch.randn(n, k, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+                for n, k in ((i, h), (i, h), (h, i))) for _ in range(copies)]
+    out = {}
+    for m in (1, 2, 8, 16, 32, 128):
+        x = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
+        res = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
+
+        def stack():
+            return [mt.dense_qmv(mt.dense_swiglu(x, g, u), d, res) for (g, u, d) in ws]
+
+        us = timed(stack, stream, max(10, args.steps // 4), args.warmup, copies)
+        total = wbytes + 2 * m * h * 3 + 4 * m * i
+        out[str(m)] = {"us_per_mlp_call": round(us, 3), "hbm_GBps": round(total / us / 1e3, 1),
+                       "weight_GBps": round(wbytes / us / 1e3, 1),
+                       "frac_of_peak": round(total / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del ws
+    return {"hidden": h, "intermediate": i, "copies": copies, "rows": out}
+
+
+def section_prefill(mt, gen, device, stream, args):
+    """INT4 prefill GEMM at M=512, Qwen2.5-1.5B up and down shapes (config 4)."""
+    out = {}
+    for name, k, n in (("up", HIDDEN, INTER), ("down", INTER, HIDDEN)):
+        copies = 4
+        ws = [make_affine(gen, device, k, n) for _ in range(copies)]
+        x = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
+        us = timed(lambda: [mt.affine_matmul(x, *w, group_size=GROUP, bits=BITS) for w in ws],
+                   stream, max(10, args.steps // 4), args.warmup, copies)
+        flops = 2 * 512 * k * n
+        out[name] = {"K": k, "N": n, "M": 512, "us": round(us, 3),
+                     "TFLOPs": round(flops / us / 1e6, 1),
+                     "frac_of_mfma_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        del ws
+    return out
+
+
+def section_ceiling(mt, device, stream, args):
+    """Streaming-read rate of one launch over distinct buffers of each byte count."""
+    from metile_amd import _lib
+
+    lib = _lib.lib()
+    sink = torch.empty(65536, dtype=torch.int32, device=device)
+    out = {}
+    for label, nbytes in (("7.7MB", 7_762_432), ("15.5MB", 15_503_872), ("23.2MB", 23_224_320),
+                          ("100.7MB", 100_663_296)):
+        copies = copies_for(nbytes)
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=device) for _ in range(copies)]
+        for b in bufs:
+            b.fill_(1)
+        best = None
+        for blocks in (256, 512, 1024):
+            def run():
+                for b in bufs:
+                    _lib.check(lib.mt_stream_read(b.data_ptr(), nbytes, sink.data_ptr(), blocks,
+                                                  torch.cuda.current_stream(device).cuda_stream))
+                return [sink]
+
+            with torch.cuda.stream(stream):
+                run()
+                torch.cuda.synchronize()
+                g = capture(run, stream)
+                us = time_graph(g, stream, max(10, args.steps // 4), args.warmup) * 1e3 / copies
+            if best is None or us < best[0]:
+                best = (us, blocks)
+        out[label] = {"us": round(best[0], 3), "GBps": round(nbytes / best[0] / 1e3, 1),
+                      "blocks": best[1]}
+        del bufs
+    return out
 
 
 def cpu_baseline(budget_s=12.0):
@@ -117,6 +291,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the other configs and the read ceiling")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the hot path runs on a single MI355X and this "
@@ -129,74 +305,20 @@ def main():
     torch.cuda.set_device(device)
     gen = torch.Generator(device=device)
     gen.manual_seed(1234)
-    layers = [make_layer(gen, device) for _ in range(LAYERS)]
     stream = torch.cuda.Stream(device)
 
-    rows_out = {}
-    step_ms = None
-    kernel = {}
     with torch.cuda.stream(stream):
-        for m in ROWS:
-            x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
-            res = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
-            outs = [torch.empty(m, HIDDEN, dtype=torch.bfloat16, device=device)
-                    for _ in range(LAYERS)]
+        rows_out, kernel, step_ms = section_mlp(mt, gen, device, stream, args)
+        configs, ceiling = {}, None
+        if not args.headline_only:
+            configs["0"] = section_qmv(mt, gen, device, stream, args, HIDDEN, INTER, 4, ROWS)
+            configs["2"] = section_dense(mt, gen, device, stream, args)
+            configs["3"] = section_qmv(mt, gen, device, stream, args, 5120, 17408, 8, (1, 8, 16))
+            configs["4"] = section_prefill(mt, gen, device, stream, args)
+    if not args.headline_only:
+        ceiling = section_ceiling(mt, device, stream, args)
 
-            def run_stack():
-                for li, (g, u, d) in enumerate(layers):
-                    outs[li] = mt.affine_mlp(x, g, u, d, group_size=GROUP, bits=BITS,
-                                             residual=res)
-
-            run_stack()  # eager: allocates the workspace for this stream before capture
-            torch.cuda.synchronize()
-            eager = [o.clone() for o in outs]
-            graph = capture(run_stack, stream)
-            graph.replay()
-            torch.cuda.synchronize()
-            for a, b in zip(eager, outs):
-                if not torch.equal(a.view(torch.int16), b.view(torch.int16)):
-                    raise RuntimeError(f"graph replay differs from eager at M={m}")
-            steps = args.steps if m == 1 else max(10, args.steps // 4)
-            ms = time_graph(graph, stream, steps, args.warmup)
-            per_call_us = ms * 1e3 / LAYERS
-            wbytes = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
-            rows_out[str(m)] = {
-                "us_per_mlp_call": round(per_call_us, 3),
-                "hbm_GBps": round(mlp_bytes(m) / (per_call_us * 1e-6) / 1e9, 1),
-                "weight_GBps": round(wbytes / (per_call_us * 1e-6) / 1e9, 1),
-                "frac_of_peak": round(mlp_bytes(m) / (per_call_us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                                      4),
-            }
-            if m == 1:
-                step_ms = ms
-                # dominant kernel alone: 28 back-to-back fused SwiGLU launches
-                hs = [torch.empty(m, INTER, dtype=torch.bfloat16, device=device)
-                      for _ in range(LAYERS)]
-
-                def run_swiglu():
-                    for li, (g, u, _d) in enumerate(layers):
-                        hs[li] = mt.affine_swiglu(x, *g, *u, group_size=GROUP, bits=BITS)
-
-                def run_down():
-                    for li, (_g, _u, d) in enumerate(layers):
-                        outs[li] = mt.affine_qmv(hs[li], *d, group_size=GROUP, bits=BITS,
-                                                 residual=res)
-
-                run_swiglu()
-                run_down()
-                torch.cuda.synchronize()
-                g_sw = capture(run_swiglu, stream)
-                g_dn = capture(run_down, stream)
-                sw_us = time_graph(g_sw, stream, args.steps, args.warmup) * 1e3 / LAYERS
-                dn_us = time_graph(g_dn, stream, args.steps, args.warmup) * 1e3 / LAYERS
-                sw_bytes = 2 * proj_weight_bytes(HIDDEN, INTER) + 2 * m * HIDDEN + 2 * m * INTER
-                dn_bytes = proj_weight_bytes(INTER, HIDDEN) + 2 * m * INTER + 4 * m * HIDDEN
-                kernel = {
-                    "swiglu_us": sw_us, "swiglu_bytes": sw_bytes,
-                    "down_us": dn_us, "down_bytes": dn_bytes,
-                }
-
-    achieved = kernel["swiglu_bytes"] / (kernel["swiglu_us"] * 1e-6) / 1e9
+    achieved = kernel["swiglu_bytes"] / kernel["swiglu_us"] / 1e3
     value = LAYERS * mlp_bytes(1) / (step_ms * 1e-3) / 1e9
     result = {
         "metric": "INT4 qmv achieved HBM GB/s (% of peak) at M=1..32; us/call for SwiGLU MLP",
@@ -227,10 +349,15 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
             "avg_kernel_us": round(kernel["swiglu_us"], 3),
+            "bytes_per_launch": kernel["swiglu_bytes"],
             "down_avg_kernel_us": round(kernel["down_us"], 3),
-            "down_achieved": round(kernel["down_bytes"] / (kernel["down_us"] * 1e-6) / 1e9, 1),
+            "down_achieved": round(kernel["down_bytes"] / kernel["down_us"] / 1e3, 1),
         },
     }
+    if configs:
+        result["configs"] = configs
+    if ceiling:
+        result["ceiling"] = {"stream_read_one_launch": ceiling}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
     print(json.dumps(result), flush=True)

@@ -123,6 +123,14 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
                           int K, int N, int dtype, void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* ---- measurement -------------------------------------------------------------------------- */
+
+/* Reads `bytes` from `p` with `blocks` workgroups of 16-byte loads and writes one word per
+ * block to `sink` (at least `blocks` words): the streaming-read ceiling of one launch. No
+ * counterpart entry point in the reference; it is the analogue of its measured
+ * streaming-read constant (metile/target/agx.py:38). */
+int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

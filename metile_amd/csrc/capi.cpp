@@ -11,6 +11,7 @@
 #include "affine_qmv.h"
 #include "dense_qmv.h"
 #include "affine_gemm.h"
+#include "stream_read.h"
 
 namespace {
 
@@ -391,6 +392,16 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
   p.steps_per_split = g.steps_per_split;
   const hipError_t e = mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "mt_affine_gemm");
+  return MT_OK;
+}
+
+int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  if (!p || !sink || bytes == 0 || bytes >= (1ull << 31) || blocks < 1 || blocks > 65536)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "mt_stream_read: need a buffer below 2 GiB, a sink and 1..65536 blocks");
+  const hipError_t e = mt::launch_stream_read(p, (uint32_t)bytes, sink, blocks,
+                                              static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_stream_read");
   return MT_OK;
 }
 
