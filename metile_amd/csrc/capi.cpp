@@ -37,8 +37,9 @@ constexpr int kRowChunk = 32;  // rows per small-row dispatch
 constexpr size_t kCounterBytes = 64 * 1024;
 constexpr int kMaxStrips = (int)(kCounterBytes / 4);
 
-// Split-K plan of the small-row kernel for one (K, N): about 1.5 workgroups per CU, with at
-// least 16 K steps (4 per wave) in each split. Depends only on K and N.
+// Split-K plan of the small-row kernel for one (K, N): about one workgroup per CU (splitting
+// further costs more in partial-sum traffic and reduction than it gains in parallelism), with
+// at least 16 K steps in each split. Depends only on K and N.
 struct Plan {
   int ksplit;
   int steps_per_split;
@@ -47,7 +48,7 @@ struct Plan {
 Plan plan_qmv(int K, int N) {
   const int steps = K / 64;
   const int strips = N / 32;
-  int ksplit = (384 + strips / 2) / strips;
+  int ksplit = (256 + strips / 2) / strips;
   const int max_split = steps / 16 > 0 ? steps / 16 : 1;
   if (ksplit > max_split) ksplit = max_split;
   // Each split covers at most kMaxGroupsPerSplit - 1 groups of 64 (one more may straddle).
@@ -62,6 +63,14 @@ Plan plan_qmv(int K, int N) {
   p.steps_per_split = (steps + ksplit - 1) / ksplit;
   p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
   return p;
+}
+
+// Activation-staged small-row kernel where it fits (M <= 16 and a bounded K range per
+// split); METILE_AMD_QMV_PATH=reg forces the register-staged kernel (for comparisons).
+bool use_lds_path(int rows, int steps_per_split, int nproj) {
+  const char* env = std::getenv("METILE_AMD_QMV_PATH");
+  if (env && std::string(env) == "reg") return false;
+  return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj);
 }
 
 size_t qmv_workspace(int M, int K, int N, int nproj) {
@@ -133,7 +142,9 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.group_shift = __builtin_ctz((unsigned)(group_size / 64));
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
-    const hipError_t e = mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
+    const hipError_t e = use_lds_path(rows, plan.steps_per_split, nproj)
+                             ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
+                             : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
     if (e != hipSuccess) return hip_fail(e, op);
   }
   return MT_OK;

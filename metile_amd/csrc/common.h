@@ -115,6 +115,43 @@ __device__ __forceinline__ u32x4 unpack_u4(uint32_t w) {
   return out;
 }
 
+// 8 nibbles of one word -> 8 values in the paired order (0,4,1,5,2,6,3,7): element pair i of
+// the result holds codes i and i + 4, which one AND-OR per pair produces (a shift and an
+// AND-OR for i > 0). The other MFMA operand must be supplied in the same order.
+// The mask and the exponent pattern are held in registers (see paired_consts) so that each
+// AND-OR is one v_and_or_b32, which as a three-operand instruction takes no literals here.
+struct PairedConsts {
+  uint32_t mask;
+  uint32_t magic;
+};
+
+template <int DT>
+__device__ __forceinline__ PairedConsts paired_consts() {
+  PairedConsts c{0x000F000Fu, (DT == kBF16) ? 0x43004300u : 0x64006400u};
+  __asm__("" : "+v"(c.mask));
+  __asm__("" : "+v"(c.magic));
+  return c;
+}
+
+__device__ __forceinline__ u32x4 unpack_u4_paired(uint32_t w, PairedConsts c) {
+  u32x4 out;
+  out.x = (w & c.mask) | c.magic;
+  out.y = ((w >> 4) & c.mask) | c.magic;
+  out.z = ((w >> 8) & c.mask) | c.magic;
+  out.w = ((w >> 12) & c.mask) | c.magic;
+  return out;
+}
+
+// Eight 16-bit values in K order (two per uint32) -> the paired order (0,4,1,5,2,6,3,7).
+__device__ __forceinline__ u32x4 pair_order(u32x4 v) {
+  u32x4 out;
+  out.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+  out.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+  out.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  out.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  return out;
+}
+
 // 4 bytes of one word -> 4 values in K order, packed two per uint32.
 template <int DT>
 __device__ __forceinline__ u32x2 unpack_u8(uint32_t w) {
