@@ -28,19 +28,26 @@ struct QmvParams {
 hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,
                              hipStream_t stream);
 
-// ---- activation-staged small-row variant (M <= 16) -------------------------------------
+// LDS row (in 32-bit words) of one column's scales or biases over a split's groups.
+constexpr int kSbRowWords = kMaxGroupsPerSplit / 2 + 2;
+
+// ---- activation-staged small-row kernels (M <= 16) --------------------------------------
 // Eight waves per workgroup; the workgroup's activation rows for its K range live in LDS.
 constexpr int kQmvLdsWaves = 8;
 constexpr int kQmvLdsMaxRows = 16;
+// Dynamic LDS bound of one workgroup: two workgroups still share a CU's 160 KiB.
+constexpr uint32_t kQmvLdsMaxBytes = 80u * 1024u;
 
 // 16-byte activation chunks each thread stages (M * steps_per_split * 8 chunks in all).
 __host__ __device__ constexpr int qmv_lds_chunk_iters(int mrows) { return mrows <= 8 ? 5 : 8; }
 
-// Dynamic LDS of one workgroup, in bytes: activation rows [M + 1][steps_per_split * 64 + 8]
-// (row M is all zeros and stands in for rows M..31 of the MFMA tile), per-step row sums
-// [steps_per_split][mrows] (fp32). The cross-wave reduction buffer [waves][nproj][mrows][33]
-// (fp32) reuses the same space after the K loop.
+// Dynamic LDS of one workgroup, byte offsets: scales and biases [2 nproj][32][kSbRowWords]
+// (32-bit words), activation rows [M + 1][steps_per_split * 64 + 8] (16-bit; row M is all
+// zeros and stands in for rows M..31 of the MFMA tile), per-step row sums
+// [steps_per_split][mrows] (fp32). After the K loop the cross-wave reduction buffer
+// [waves][nproj][mrows][33] (fp32) reuses the space from offset 0.
 struct QmvLdsLayout {
+  uint32_t x;
   uint32_t zero;
   uint32_t xsum;
   uint32_t bytes;
@@ -50,7 +57,8 @@ __host__ __device__ inline QmvLdsLayout qmv_lds_layout(int M, int steps_per_spli
                                                        int nproj) {
   QmvLdsLayout l;
   const uint32_t row = (uint32_t)(steps_per_split * 64 + 8) * 2u;
-  l.zero = (uint32_t)M * row;
+  l.x = (uint32_t)(2 * nproj * 32 * kSbRowWords) * 4u;
+  l.zero = l.x + (uint32_t)M * row;
   l.xsum = l.zero + row;
   const uint32_t staged = l.xsum + (uint32_t)(steps_per_split * mrows) * 4u;
   const uint32_t red = (uint32_t)(kQmvLdsWaves * nproj * mrows * 33) * 4u;
@@ -58,13 +66,29 @@ __host__ __device__ inline QmvLdsLayout qmv_lds_layout(int M, int steps_per_spli
   return l;
 }
 
-// Whether the activation-staged variant takes a call of M rows split into K ranges of
-// steps_per_split 64-wide steps (its staging must fit in the per-thread chunk budget and in
-// 64 KiB of dynamic LDS).
+// Whether the activation-staged kernels take M rows split into K ranges of steps_per_split
+// 64-wide steps (the staging must fit the per-thread chunk budget and kQmvLdsMaxBytes).
 bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj);
 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,
                                  hipStream_t stream);
+
+// One-launch quantized MLP, y = down(silu(gate x) * up x) (+ residual), for M <= 16.
+// Workgroups [0, blocks_up) compute the gate/up strips of `up` (its y is the hidden
+// activation h in the workspace) and publish each finished hidden strip; the remaining
+// workgroups compute the down strips of `down` (x = h) and start their K range once every
+// hidden strip in it is published. Workgroups are dispatched in index order, so every
+// gate/up workgroup has started before any down workgroup waits; the waits are bounded.
+struct MlpLink {
+  uint32_t* ready;  // [down splits] hidden strips published in each down split's K range
+  uint32_t* done;   // down workgroups finished; the last one clears ready[] and done
+  int hstrips_per_split;
+  int down_blocks;
+  int prefetch_at;  // published strips of its split before a down workgroup requests codes
+};
+
+hipError_t launch_affine_mlp_fused(const QmvParams& up, const QmvParams& down,
+                                   const MlpLink& link, int bits, int dtype, hipStream_t stream);
 
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                                     float* out, int N, int K, int G, int bits, int dtype,

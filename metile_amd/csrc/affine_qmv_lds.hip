@@ -1,0 +1,504 @@
+// Activation-staged small-row affine projections (M <= 16) and the one-launch quantized MLP,
+// for gfx950.
+//
+// Same contract as affine_qmv.hip: y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/G] + b[n, k/G])
+// (reference semantics kernels/affine_qmv.py:4-54; residual and SwiGLU epilogues
+// kernels/affine_qmv.py:124-132,204-214; the MLP composition of mlx_affine_mlp_executor,
+// metile/backends/mlx_quantized.py:1770-1832), with the same work split (32-column strips x
+// K splits, four to eight K steps per wave), scale staging, fixed-order cross-wave reduction and
+// deterministic split-K protocol. What differs from affine_qmv_kernel:
+//  * The workgroup's activation rows for its K range are loaded once and parked in LDS. For
+//    4-bit codes each group of 8 elements is stored in the paired order (0,4,1,5,2,6,3,7), so
+//    a word of codes unpacks with one AND-OR per pair of codes (unpack_u4_paired) and the MFMA
+//    A operand of a K slice is one 16-byte LDS read. Lanes of rows >= M read a zero row.
+//  * The per-row activation sum of every K step (the factor of the bias term) is summed once
+//    while staging: eight lanes hold the eight 16-byte chunks of one (row, step) and combine
+//    their sums with three lane exchanges.
+//  * The register ring holds codes only, so a wave needs about half the registers and a
+//    workgroup runs eight waves.
+//
+// The one-launch MLP runs the gate/up strips and the down strips as two sets of workgroups of
+// one grid. A gate/up workgroup that finishes a hidden strip (32 columns of
+// h = silu(gate x) * up x, rounded to the activation type) writes it with device-coherent
+// stores and counts it into ready[] of the down K split that reads it. A down workgroup issues
+// its scale and code loads first, then waits until its K split's hidden strips are all counted,
+// then reads h with device-coherent loads. The last down workgroup to finish clears the
+// hand-off counters, so every call starts from zero. This removes the second launch's fixed
+// latency and lets the down weights stream while the gate/up strips are still computing.
+#include "common.h"
+#include "affine_qmv.h"
+
+namespace mt {
+namespace {
+
+enum Role : int { kPlain = 0, kGateUp = 1, kDown = 2 };
+
+// Code stages each wave requests before the workgroup parks its scales and activations.
+constexpr int kQmvEarlyStages = 2;
+
+// Polls of the hand-off counter before a down workgroup gives up (about 60 ms); its outputs
+// are then NaN, so a broken hand-off is loud and the grid still drains.
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+template <int DT>
+__device__ __forceinline__ uint16_t quiet_nan() {
+  return DT == kBF16 ? (uint16_t)0x7FC0u : (uint16_t)0x7E00u;
+}
+
+// One workgroup's share: output strip `strip` (32 columns) over K split `split`.
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE>
+__device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, const int split,
+                                         unsigned char* __restrict__ dyn, int& flag,
+                                         const MlpLink& link) {
+  constexpr int WAVES = kQmvLdsWaves;
+  constexpr int kThreads = WAVES * 64;
+  constexpr float kOff = CodeOffset<BITS, DT>::value;
+  constexpr int kRegs = MROWS / 2;
+  constexpr int kArrays = 2 * NPROJ;
+  constexpr int kXIters = qmv_lds_chunk_iters(MROWS);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int M = p.M, K = p.K, N = p.N;
+  const int steps_total = K >> 6;
+  const int s_beg = split * p.steps_per_split;
+  const int s_end = min(steps_total, s_beg + p.steps_per_split);
+  const int steps_here = s_end - s_beg;
+  const int per_wave = (steps_here + WAVES - 1) / WAVES;
+  const int w_beg = s_beg + wave * per_wave;
+  const int w_end = min(s_end, w_beg + per_wave);
+  const int gshift = p.group_shift;
+  // Scale rows are staged from the 32-bit word holding group g_beg; a row whose element
+  // index (row * groups_per_row + g_beg) is odd starts one 16-bit element into its segment.
+  const int g_beg = s_beg >> gshift;
+  const int g_last = (s_end - 1) >> gshift;
+  const int nwords = (g_last - g_beg + 1) / 2 + 1;
+  const QmvLdsLayout lay = qmv_lds_layout(M, p.steps_per_split, MROWS, NPROJ);
+  const int xstride = p.steps_per_split * 64 + 8;  // staged row stride, elements
+  uint32_t* sb = reinterpret_cast<uint32_t*>(dyn);  // [kArrays][32][kSbRowWords]
+  float* xsum = reinterpret_cast<float*>(dyn + lay.xsum);  // [steps_per_split][MROWS]
+
+  const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
+  const int groups_per_row = K / p.G;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  __amdgpu_buffer_rsrc_t rw[NPROJ];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr) rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * row_bytes);
+
+  // ---- scales and biases: thread t copies 16-byte quads of row t % 32 of every array -----
+  constexpr int kQuadsPerRow = (kSbRowWords + 3) / 4;
+  constexpr int kSbIters = (kQuadsPerRow + kThreads / 32 - 1) / (kThreads / 32);
+  const int sb_row = tid & 31;
+  const int sb_q0 = tid >> 5;
+  u32x4 sbv[kArrays][kSbIters];
+#pragma unroll
+  for (int a = 0; a < kArrays; ++a) {
+    const uint16_t* src = (a & 1) ? p.b[a >> 1] : p.s[a >> 1];
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)N * groups_per_row * 2u);
+    const uint32_t base = (((uint32_t)(strip * 32 + sb_row) * groups_per_row + g_beg) * 2u) & ~3u;
+#pragma unroll
+    for (int k = 0; k < kSbIters; ++k) {
+      const int q = sb_q0 + k * (kThreads / 32);
+      sbv[a][k] = load16(r, 4 * q < nwords ? base + 16u * q : kOOB);
+    }
+  }
+
+  // ---- activation chunks: chunk c = row * cpr + cc holds elements [8 cc, 8 cc + 8) --------
+  const int cpr = steps_here * 8;
+  const int nchunks = M * cpr;
+  const float inv_cpr = 1.0f / (float)cpr;
+  u32x4 xv[kXIters];
+  auto issue_x = [&]() {
+#pragma unroll
+    for (int i = 0; i < kXIters; ++i) {
+      const int c = tid + i * kThreads;
+      const int row = (int)(((float)c + 0.5f) * inv_cpr);
+      const int cc = c - row * cpr;
+      const uint32_t off =
+          c < nchunks ? ((uint32_t)row * K + (uint32_t)(s_beg * 64 + cc * 8)) * 2u : kOOB;
+      xv[i] = ROLE == kDown ? load16_device(rx, off) : load16(rx, off);
+    }
+  };
+  if constexpr (ROLE != kDown) issue_x();
+
+  // ---- code ring ---------------------------------------------------------------------------
+  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + (uint32_t)h * 4u * BITS;
+  typedef u32x4 StageW[NPROJ][BITS / 4];
+  StageW ring[STAGES];
+  auto load_stage = [&](StageW& S, int st) {
+    const bool ok = st < w_end;
+    const uint32_t woff = ok ? w_row + (uint32_t)st * 8u * BITS : kOOB;
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int v = 0; v < BITS / 4; ++v) S[pr][v] = load16(rw[pr], ok ? woff + 16u * v : kOOB);
+  };
+  // ---- down workgroups: wait until the hidden strips of this K split are published --------
+  // The codes are requested once link.prefetch_at strips of the split are published (0: at
+  // once), the hidden activation once all are.
+  bool timed_out = false;
+  auto wait_ready = [&](uint32_t target) {
+    if (tid == 0) {
+      uint32_t spins = 0;
+      while (__hip_atomic_load(&link.ready[split], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
+             target) {
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins == kSpinLimit) break;
+      }
+      flag = spins == kSpinLimit;
+    }
+    __syncthreads();
+    return flag != 0;
+  };
+  const uint32_t need = (uint32_t)(2 * steps_here);
+  if constexpr (ROLE == kDown) {
+    if (link.prefetch_at > 0) timed_out = wait_ready(min((uint32_t)link.prefetch_at, need));
+  }
+  // The first EARLY stages are requested before the scales and activations are parked, the
+  // rest after: requests behind the bulk of the grid's code stream would otherwise hold up
+  // the data every K step depends on.
+  constexpr int kEarly = (ROLE == kDown || EARLY > STAGES) ? STAGES : EARLY;
+#pragma unroll
+  for (int d = 0; d < kEarly; ++d) load_stage(ring[d], w_beg + d);
+  if constexpr (ROLE == kDown) {
+    if (!timed_out) timed_out = wait_ready(need);
+    issue_x();
+  }
+
+  // ---- park scales, biases and activations in LDS; per-step row sums ----------------------
+#pragma unroll
+  for (int a = 0; a < kArrays; ++a)
+#pragma unroll
+    for (int k = 0; k < kSbIters; ++k) {
+      const int q = sb_q0 + k * (kThreads / 32);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (4 * q + c < kSbRowWords) sb[(a * 32 + sb_row) * kSbRowWords + 4 * q + c] = sbv[a][k][c];
+    }
+#pragma unroll
+  for (int i = 0; i < kXIters; ++i) {
+    const int c = tid + i * kThreads;
+    // Every aligned group of 8 chunks (one row and step) is wholly below nchunks or wholly
+    // above, so the lane exchanges stay inside active groups.
+    if (i * kThreads < nchunks) {
+      const int row = (int)(((float)c + 0.5f) * inv_cpr);
+      const int cc = c - row * cpr;
+      float s = sum8<DT>(xv[i], 0.0f);
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      s += __shfl_xor(s, 4);
+      if (c < nchunks) {
+        const u32x4 v = (BITS == 4) ? pair_order(xv[i]) : xv[i];
+        *reinterpret_cast<u32x4*>(dyn + lay.x + ((uint32_t)row * xstride + cc * 8) * 2u) = v;
+        if ((cc & 7) == 0) xsum[(cc >> 3) * MROWS + row] = s;
+      }
+    }
+  }
+  // Row sums of rows M..MROWS-1 and the zero row.
+  for (int idx = tid; idx < steps_here * MROWS; idx += kThreads)
+    if ((idx % MROWS) >= M) xsum[idx] = 0.0f;
+  for (int q = tid; q < xstride / 8; q += kThreads)
+    *reinterpret_cast<u32x4*>(dyn + lay.zero + 16u * q) = (u32x4){0u, 0u, 0u, 0u};
+  __syncthreads();
+#pragma unroll
+  for (int d = kEarly; d < STAGES; ++d) load_stage(ring[d], w_beg + d);
+
+  // ---- K loop --------------------------------------------------------------------------------
+  float acc[NPROJ][kRegs];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r) acc[pr][r] = 0.0f;
+
+  const f32x16 zero16 = (f32x16){0};
+  const PairedConsts pc = paired_consts<DT>();
+  const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(sb);
+  const int sb_shift = ((strip * 32 + j) * groups_per_row + g_beg) & 1;
+  // A operand of lane (j, h): row j (the zero row for j >= M), elements [32 h, 32 h + 32) of
+  // each step's 64.
+  const uint32_t a_base = lay.x + ((uint32_t)min(j, M) * xstride + 32u * h) * 2u;
+  for (int s0 = w_beg; s0 < w_end; s0 += STAGES) {
+#pragma unroll
+    for (int d = 0; d < STAGES; ++d) {
+      StageW& S = ring[d];
+      const int st = s0 + d;
+      if (st < w_end) {
+        const int sl = st - s_beg;
+        const unsigned char* ap = dyn + a_base + (uint32_t)sl * 128u;
+        u32x4 a[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[e] = *reinterpret_cast<const u32x4*>(ap + 16 * e);
+        float xs[kRegs];
+#pragma unroll
+        for (int q = 0; q < kRegs / 4; ++q) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(&xsum[sl * MROWS + 8 * q + 4 * h]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[4 * q + r] = v[r];
+        }
+        const int gl = (st >> gshift) - g_beg + sb_shift;
+#pragma unroll
+        for (int pr = 0; pr < NPROJ; ++pr) {
+          f32x16 t;
+          if constexpr (BITS == 4) {
+            t = mfma32<DT>(a[0], unpack_u4_paired(S[pr][0][0], pc), zero16);
+#pragma unroll
+            for (int e = 1; e < 4; ++e) t = mfma32<DT>(a[e], unpack_u4_paired(S[pr][0][e], pc), t);
+          } else {
+            t = mfma32<DT>(a[0], code_frag<BITS, DT>(S[pr], 0), zero16);
+#pragma unroll
+            for (int e = 1; e < 4; ++e) t = mfma32<DT>(a[e], code_frag<BITS, DT>(S[pr], e), t);
+          }
+          const float sf = act_to_f32<DT>(sb16[((2 * pr) * 32 + j) * 2 * kSbRowWords + gl]);
+          const float bf = act_to_f32<DT>(sb16[((2 * pr + 1) * 32 + j) * 2 * kSbRowWords + gl]);
+          const float bp = __builtin_fmaf(-kOff, sf, bf);
+#pragma unroll
+          for (int r = 0; r < kRegs; ++r) {
+            acc[pr][r] = __builtin_fmaf(sf, t[r], acc[pr][r]);
+            acc[pr][r] = __builtin_fmaf(bp, xs[r], acc[pr][r]);
+          }
+        }
+      }
+      load_stage(S, st + STAGES);
+    }
+  }
+
+  // ---- cross-wave reduction (fixed order); the buffer reuses the staged data -------------
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(dyn);  // [WAVES][NPROJ][MROWS][33]
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int r = 0; r < kRegs; ++r)
+      red[((wave * NPROJ + pr) * MROWS + mfma32_row(r, h)) * 33 + j] = acc[pr][r];
+  __syncthreads();
+
+  auto reduce = [&](int pr, int i, int c) {
+    float v = red[(pr * MROWS + i) * 33 + c];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) v += red[((w * NPROJ + pr) * MROWS + i) * 33 + c];
+    return v;
+  };
+
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)M * N * 2u);
+  // Final value of output (i, c) of this strip from its K sums v[].
+  auto finish = [&](int i, int c, const float (&v)[NPROJ]) {
+    const size_t oi = (size_t)i * N + strip * 32 + c;
+    float out;
+    if constexpr (NPROJ == 2) {
+      out = silu_mul(v[0], v[1]);
+    } else {
+      out = v[0];
+      if (p.residual) out += act_to_f32<DT>(p.residual[oi]);
+    }
+    const uint16_t o16 = timed_out ? quiet_nan<DT>() : f32_to_act<DT>(out);
+    if constexpr (ROLE == kGateUp) {
+      store2_device(ry, (uint32_t)oi * 2u, o16);
+    } else {
+      p.y[oi] = o16;
+    }
+  };
+  // Gate/up: after this workgroup's stores of a finished hidden strip have completed, count
+  // the strip into its down split.
+  auto publish = [&]() {
+    if constexpr (ROLE == kGateUp) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_fetch_add(&link.ready[strip / link.hstrips_per_split], 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  // Down: count this workgroup out; the last one clears the hand-off counters.
+  auto retire = [&]() {
+    if constexpr (ROLE == kDown) {
+      if (tid == 0) {
+        const unsigned prev =
+            __hip_atomic_fetch_add(link.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (prev == (unsigned)(link.down_blocks - 1)) {
+          for (int b = 0; b < p.ksplit; ++b)
+            __hip_atomic_store(&link.ready[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(link.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  };
+
+  const int outs = M * 32;
+  if (p.ksplit == 1) {
+    for (int o = tid; o < outs; o += kThreads) {
+      float v[NPROJ];
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr) v[pr] = reduce(pr, o >> 5, o & 31);
+      finish(o >> 5, o & 31, v);
+    }
+    publish();
+    retire();
+    return;
+  }
+
+  // ---- split-K: publish partials, last workgroup of the strip finishes -------------------
+  // Partials are written and read with device-scope relaxed atomic accesses, which the gfx950
+  // memory model makes coherent across the chip's L2 slices without any cache-wide writeback
+  // or invalidate. Each wave waits for its stores to complete before the barrier, so every
+  // partial of this workgroup is visible before the arrival counter moves.
+  const size_t plane = (size_t)M * N;
+  for (int o = tid; o < outs; o += kThreads) {
+    const int i = o >> 5, c = o & 31;
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+      __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + pr) * plane + (size_t)i * N +
+                                    strip * 32 + c],
+                         reduce(pr, i, c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&p.counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag = (prev == (unsigned)(p.ksplit - 1));
+  }
+  __syncthreads();
+  if (!flag) {
+    retire();
+    return;
+  }
+  for (int o = tid; o < outs; o += kThreads) {
+    const int i = o >> 5, c = o & 31;
+    const size_t oi = (size_t)i * N + strip * 32 + c;
+    float v[NPROJ];
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr) {
+      float sacc = 0.0f;
+      for (int sp = 0; sp < p.ksplit; ++sp)
+        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + pr) * plane + oi],
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[pr] = sacc;
+    }
+    finish(i, c, v);
+  }
+  if (tid == 0)
+    __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  publish();
+  retire();
+}
+
+// At most 128 registers, so that two eight-wave workgroups share a CU.
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES>
+__global__ __launch_bounds__(kQmvLdsWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void affine_qmv_lds_kernel(const QmvParams p) {
+  extern __shared__ __align__(16) unsigned char dyn_plain[];
+  __shared__ int flag;
+  const MlpLink none{};
+  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain>(p, blockIdx.x, blockIdx.y,
+                                                                   dyn_plain, flag, none);
+}
+
+template <int BITS, int DT, int MROWS>
+__global__ __launch_bounds__(kQmvLdsWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void affine_mlp_kernel(const QmvParams up, const QmvParams down, const MlpLink link,
+                       int blocks_up) {
+  extern __shared__ __align__(16) unsigned char dyn_mlp[];
+  __shared__ int flag;
+  constexpr int kStagesUp = BITS == 4 ? 4 : 2;
+  constexpr int kStagesDown = BITS == 4 ? 6 : 4;
+  const int id = blockIdx.x;
+  if (id < blocks_up) {
+    const int strips = up.N / 32;
+    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp>(up, id % strips,
+                                                                      id / strips, dyn_mlp, flag,
+                                                                      link);
+  } else {
+    const int strips = down.N / 32;
+    const int idd = id - blocks_up;
+    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown>(down, idd % strips,
+                                                                  idd / strips, dyn_mlp, flag,
+                                                                  link);
+  }
+}
+
+// Raises a kernel's dynamic LDS limit (64 KiB by default) to kQmvLdsMaxBytes. The launchers
+// call it once per kernel instantiation (a function-local static in each launcher template).
+hipError_t allow_lds(const void* kernel) {
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kQmvLdsMaxBytes);
+}
+
+template <int BITS, int DT, int MROWS, int NPROJ>
+hipError_t launch_lds_rows(const QmvParams& p, hipStream_t stream) {
+  constexpr int kStages = BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4);
+  const QmvLdsLayout lay = qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ);
+  const dim3 grid(p.N / 32, p.ksplit);
+  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages>;
+  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
+  if (attr != hipSuccess) return attr;
+  kernel<<<grid, dim3(kQmvLdsWaves * 64), lay.bytes, stream>>>(p);
+  return hipGetLastError();
+}
+
+template <int BITS, int DT, int NPROJ>
+hipError_t launch_lds_nproj(const QmvParams& p, hipStream_t stream) {
+  return p.M <= 8 ? launch_lds_rows<BITS, DT, 8, NPROJ>(p, stream)
+                  : launch_lds_rows<BITS, DT, 16, NPROJ>(p, stream);
+}
+
+template <int BITS, int DT>
+hipError_t launch_lds_bits_dt(const QmvParams& p, int nproj, hipStream_t stream) {
+  return nproj == 2 ? launch_lds_nproj<BITS, DT, 2>(p, stream)
+                    : launch_lds_nproj<BITS, DT, 1>(p, stream);
+}
+
+template <int BITS, int DT, int MROWS>
+hipError_t launch_mlp_rows(const QmvParams& up, const QmvParams& down, const MlpLink& link,
+                           hipStream_t stream) {
+  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2);
+  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1);
+  const int blocks_up = (up.N / 32) * up.ksplit;
+  const int blocks = blocks_up + link.down_blocks;
+  auto kernel = affine_mlp_kernel<BITS, DT, MROWS>;
+  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
+  if (attr != hipSuccess) return attr;
+  kernel<<<dim3(blocks), dim3(kQmvLdsWaves * 64), la.bytes > lb.bytes ? la.bytes : lb.bytes,
+           stream>>>(up, down, link, blocks_up);
+  return hipGetLastError();
+}
+
+template <int BITS, int DT>
+hipError_t launch_mlp_bits_dt(const QmvParams& up, const QmvParams& down, const MlpLink& link,
+                              hipStream_t stream) {
+  return up.M <= 8 ? launch_mlp_rows<BITS, DT, 8>(up, down, link, stream)
+                   : launch_mlp_rows<BITS, DT, 16>(up, down, link, stream);
+}
+
+}  // namespace
+
+bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj) {
+  if (M < 1 || M > kQmvLdsMaxRows) return false;
+  const int mrows = M <= 8 ? 8 : 16;
+  if (M * steps_per_split * 8 > qmv_lds_chunk_iters(mrows) * kQmvLdsWaves * 64) return false;
+  return qmv_lds_layout(M, steps_per_split, mrows, nproj).bytes <= kQmvLdsMaxBytes;
+}
+
+hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,
+                                 hipStream_t stream) {
+  if (bits == 4) {
+    return dtype == kBF16 ? launch_lds_bits_dt<4, kBF16>(p, nproj, stream)
+                          : launch_lds_bits_dt<4, kF16>(p, nproj, stream);
+  }
+  return dtype == kBF16 ? launch_lds_bits_dt<8, kBF16>(p, nproj, stream)
+                        : launch_lds_bits_dt<8, kF16>(p, nproj, stream);
+}
+
+hipError_t launch_affine_mlp_fused(const QmvParams& up, const QmvParams& down,
+                                   const MlpLink& link, int bits, int dtype, hipStream_t stream) {
+  if (bits == 4) {
+    return dtype == kBF16 ? launch_mlp_bits_dt<4, kBF16>(up, down, link, stream)
+                          : launch_mlp_bits_dt<4, kF16>(up, down, link, stream);
+  }
+  return dtype == kBF16 ? launch_mlp_bits_dt<8, kBF16>(up, down, link, stream)
+                        : launch_mlp_bits_dt<8, kF16>(up, down, link, stream);
+}
+
+}  // namespace mt

@@ -249,6 +249,63 @@ size_t gemm_workspace(int M, int K, int N) {
   return kCounterBytes + (size_t)g.ksplit * M * N * 4;
 }
 
+// ---- one-launch MLP plan ---------------------------------------------------------------
+// Gate/up keeps the small-row plan; the down projection takes as many K splits as fit beside
+// the gate/up workgroups in one resident wave of the grid (two eight-wave workgroups per CU on
+// a 256-CU part), at least what its staging limits require. Depends only on (M, H, I) and the
+// environment override, so the workspace query and the call agree.
+constexpr int kResidentWorkgroups = 512;
+
+struct MlpPlan {
+  bool fused;
+  Plan up, down;
+  size_t up_partial, down_partial, hidden, bytes;  // workspace offsets (bytes) and total
+};
+
+MlpPlan plan_mlp(int M, int H, int I) {
+  MlpPlan mp{};
+  mp.up = plan_qmv(H, I);
+  mp.down = plan_qmv(I, H);
+  // The one-launch MLP is opt-in (METILE_AMD_MLP_PATH=fused): on MI355X its hand-off chain
+  // (hidden-strip store acknowledgement, counter, coherent reload) costs several HBM round
+  // trips while the weight stream is still in flight, which measured slower than two launches.
+  const char* env = std::getenv("METILE_AMD_MLP_PATH");
+  const bool forced_split = !(env && std::string(env) == "fused");
+  const int strips_up = I / 32, strips_down = H / 32, steps_down = I / 64;
+  const int blocks_up = strips_up * mp.up.ksplit;
+  int ks = (kResidentWorkgroups - blocks_up) / strips_down;
+  if (ks > mp.down.ksplit) ks = mp.down.ksplit;
+  const int min_split = (steps_down + mt::kMaxGroupsPerSplit - 2) / (mt::kMaxGroupsPerSplit - 1);
+  if (ks < min_split) ks = min_split;
+  if (ks < 1) ks = 1;
+  Plan down{};
+  for (; ks <= steps_down; ++ks) {
+    down.steps_per_split = (steps_down + ks - 1) / ks;
+    down.ksplit = (steps_down + down.steps_per_split - 1) / down.steps_per_split;
+    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1)) break;
+  }
+  mp.fused = !forced_split && M <= mt::kQmvLdsMaxRows && ks <= steps_down &&
+             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2) &&
+             strips_up + strips_down + down.ksplit + 1 <= kMaxStrips;
+  if (mp.fused) {
+    mp.down = down;
+    mp.up_partial = kCounterBytes;
+    const size_t up_bytes =
+        mp.up.ksplit > 1 ? align_up((size_t)mp.up.ksplit * 2 * M * I * 4) : 0;
+    mp.down_partial = mp.up_partial + up_bytes;
+    const size_t down_bytes =
+        mp.down.ksplit > 1 ? align_up((size_t)mp.down.ksplit * M * H * 4) : 0;
+    mp.hidden = mp.down_partial + down_bytes;
+  } else {
+    const size_t a = qmv_workspace(M, H, I, 2);
+    const size_t b = qmv_workspace(M, I, H, 1);
+    const size_t split = align_up(a > b ? a : b);
+    mp.hidden = split > kCounterBytes ? split : kCounterBytes;
+  }
+  mp.bytes = mp.hidden + align_up((size_t)M * I * 2);
+  return mp;
+}
+
 }  // namespace
 
 extern "C" {
@@ -288,10 +345,7 @@ size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bi
   if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
       check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
     return 0;
-  const size_t a = qmv_workspace(M, H, I, 2);
-  const size_t b = qmv_workspace(M, I, H, 1);
-  const size_t split = align_up(a > b ? a : b);
-  return (split > kCounterBytes ? split : kCounterBytes) + align_up((size_t)M * I * 2);
+  return plan_mlp(M, H, I).bytes;
 }
 
 int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
@@ -308,14 +362,66 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   if (!workspace || workspace_bytes < need)
     return fail(MT_ERR_WORKSPACE, "mt_affine_mlp: workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
-  // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
-  const size_t hidden_off = need - align_up((size_t)M * I * 2);
-  void* h = static_cast<char*>(workspace) + hidden_off;
-  st = mt_affine_swiglu(x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h, M, H,
-                        I, group_size, bits, dtype, workspace, hidden_off, stream);
-  if (st) return st;
-  return mt_affine_qmv(h, down_w, down_scales, down_biases, residual, y, M, I, H, group_size,
-                       bits, dtype, workspace, hidden_off, stream);
+  if (!x || !y || !gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases ||
+      !down_w || !down_scales || !down_biases)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_mlp: null pointer");
+  const MlpPlan mp = plan_mlp(M, H, I);
+  char* ws = static_cast<char*>(workspace);
+  void* h = ws + mp.hidden;
+  if (!mp.fused) {
+    // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
+    st = mt_affine_swiglu(x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h, M,
+                          H, I, group_size, bits, dtype, workspace, mp.hidden, stream);
+    if (st) return st;
+    return mt_affine_qmv(h, down_w, down_scales, down_biases, residual, y, M, I, H, group_size,
+                         bits, dtype, workspace, mp.hidden, stream);
+  }
+  // [counters: gate/up strips | down strips | ready[] | done][gate/up partials]
+  // [down partials][hidden activation]
+  uint32_t* counters = reinterpret_cast<uint32_t*>(ws);
+  const int strips_up = I / 32, strips_down = H / 32;
+  mt::QmvParams up{}, down{};
+  up.x = static_cast<const uint16_t*>(x);
+  up.w[0] = gate_w;
+  up.w[1] = up_w;
+  up.s[0] = static_cast<const uint16_t*>(gate_scales);
+  up.s[1] = static_cast<const uint16_t*>(up_scales);
+  up.b[0] = static_cast<const uint16_t*>(gate_biases);
+  up.b[1] = static_cast<const uint16_t*>(up_biases);
+  up.y = static_cast<uint16_t*>(h);
+  up.partial = reinterpret_cast<float*>(ws + mp.up_partial);
+  up.counters = counters;
+  up.M = M;
+  up.K = H;
+  up.N = I;
+  up.ksplit = mp.up.ksplit;
+  up.steps_per_split = mp.up.steps_per_split;
+  down.x = static_cast<const uint16_t*>(h);
+  down.w[0] = down_w;
+  down.s[0] = static_cast<const uint16_t*>(down_scales);
+  down.b[0] = static_cast<const uint16_t*>(down_biases);
+  down.residual = static_cast<const uint16_t*>(residual);
+  down.y = static_cast<uint16_t*>(y);
+  down.partial = reinterpret_cast<float*>(ws + mp.down_partial);
+  down.counters = counters + strips_up;
+  down.M = M;
+  down.K = I;
+  down.N = H;
+  down.ksplit = mp.down.ksplit;
+  down.steps_per_split = mp.down.steps_per_split;
+  up.G = down.G = group_size;
+  up.group_shift = down.group_shift = __builtin_ctz((unsigned)(group_size / 64));
+  mt::MlpLink link{};
+  link.ready = counters + strips_up + strips_down;
+  link.done = link.ready + mp.down.ksplit;
+  link.hstrips_per_split = 2 * mp.down.steps_per_split;
+  link.down_blocks = strips_down * mp.down.ksplit;
+  link.prefetch_at = 0;
+  if (const char* env = std::getenv("METILE_AMD_MLP_PREFETCH_AT")) link.prefetch_at = std::atoi(env);
+  const hipError_t e = mt::launch_affine_mlp_fused(up, down, link, bits, dtype,
+                                                   static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_affine_mlp");
+  return MT_OK;
 }
 
 int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,

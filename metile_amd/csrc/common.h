@@ -47,6 +47,18 @@ __device__ __forceinline__ uint16_t load2(__amdgpu_buffer_rsrc_t r, uint32_t off
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
 
+// Device-coherent forms (cache policy sc1, device scope: the same accesses that device-scope
+// relaxed atomics compile to), for data written by other workgroups of the same launch, which
+// may run on another XCD with its own L2.
+constexpr int kDeviceScope = 16;
+__device__ __forceinline__ u32x4 load16_device(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kDeviceScope);
+}
+__device__ __forceinline__ void store2_device(__amdgpu_buffer_rsrc_t r, uint32_t off,
+                                              uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kDeviceScope);
+}
+
 // ---- 16-bit float conversions ----------------------------------------------------------
 
 template <int DT>
@@ -168,6 +180,20 @@ __device__ __forceinline__ u32x2 unpack_u8(uint32_t w) {
     out.y = __builtin_amdgcn_perm(f3, f2, 0x07060302u);
   }
   return out;
+}
+
+// B operand of MFMA e (K slice [8e, 8e+8) of a lane's 32 K, natural order) as 8 exact 16-bit
+// floats, from the lane's 16 (4-bit) or 32 (8-bit) bytes of codes.
+template <int BITS, int DT>
+__device__ __forceinline__ u32x4 code_frag(const u32x4 (&w)[BITS / 4], int e) {
+  if constexpr (BITS == 4) {
+    return unpack_u4<DT>(w[0][e]);
+  } else {
+    const u32x4 src = w[e >> 1];
+    const u32x2 lo = unpack_u8<DT>((e & 1) ? src.z : src.x);
+    const u32x2 hi = unpack_u8<DT>((e & 1) ? src.w : src.y);
+    return (u32x4){lo.x, lo.y, hi.x, hi.y};
+  }
 }
 
 // The two 16-bit floats of a packed pair, widened to fp32 (element 0 is the low half).

@@ -164,11 +164,13 @@ def affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_s
 
 
 def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
-    """``down(swiglu(values)) (+ residual)`` in two kernels through one C-ABI call.
+    """``down(swiglu(values)) (+ residual)`` through one C-ABI call: one kernel launch for up
+    to 16 rows (gate/up and down workgroups of one grid, handing the hidden activation over
+    through the workspace), two launches above that.
 
     ``gate``/``up``/``down`` are ``(weight, scales, biases)`` triples; gate/up ``[I, H]``,
     down ``[H, I]``. The hidden activation is rounded to the activation dtype between the two
-    kernels, as the reference executor does (``metile/backends/mlx_quantized.py:1829-1830``).
+    projections, as the reference executor does (``metile/backends/mlx_quantized.py:1829-1830``).
     """
     gw, gs, gb = gate
     uw, us, ub = up
