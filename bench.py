@@ -118,7 +118,8 @@ def section_mlp(mt, gen, device, stream, args):
     layers = [make_layer(gen, device) for _ in range(LAYERS)]
     wbytes = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
     rows_out, kernel, step_ms = {}, {}, None
-    for m in ROWS:
+    rows = sorted({1, *(int(v) for v in args.rows.split(","))})
+    for m in rows:
         x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
         res = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
 
@@ -249,6 +250,47 @@ def section_ceiling(mt, device, stream, args):
     return out
 
 
+def traffic_probe(mt, gen, device, args):
+    """Eager launches for the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then
+    WRITE_SIZE): a plain 256 MiB device copy (the calibration kernel of known size), then the
+    headline SwiGLU and down kernels over the 28-layer stack, three passes each."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(3)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    layers = [make_layer(gen, device) for _ in range(LAYERS)]
+    x = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    res = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    hs = [torch.randn(1, INTER, generator=gen, device=device).to(torch.bfloat16)
+          for _ in range(LAYERS)]
+    for _ in range(3):
+        for g, u, _d in layers:
+            mt.affine_swiglu(x, *g, *u, group_size=GROUP, bits=BITS)
+        for h, (_g, _u, d) in zip(hs, layers):
+            mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
+    torch.cuda.synchronize()
+    print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20}), flush=True)
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "affine_qmv_lds_swiglu_m1_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed counter summary (the
+    line ``traffic_bytes_per_launch: N``), or None when that summary is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
 def cpu_baseline(budget_s=12.0):
     """NumPy oracle (variant A: unpack + dequantize + fp32 BLAS every call) on one layer MLP at
     M=1, on this host's cores, for about ``budget_s`` seconds."""
@@ -293,6 +335,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the other configs and the read ceiling")
+    ap.add_argument("--rows", default=",".join(str(m) for m in ROWS),
+                    help="comma-separated row counts of the headline MLP (default: all)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only the eager launches profiled by the HBM-traffic counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the hot path runs on a single MI355X and this "
@@ -306,6 +352,9 @@ def main():
     gen = torch.Generator(device=device)
     gen.manual_seed(1234)
     stream = torch.cuda.Stream(device)
+    if args.traffic_probe:
+        traffic_probe(mt, gen, device, args)
+        return
 
     with torch.cuda.stream(stream):
         rows_out, kernel, step_ms = section_mlp(mt, gen, device, stream, args)
@@ -347,7 +396,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "avg_kernel_us": round(kernel["swiglu_us"], 3),
             "bytes_per_launch": kernel["swiglu_bytes"],
             "down_avg_kernel_us": round(kernel["down_us"], 3),
