@@ -23,6 +23,8 @@ struct QmvParams {
   int group_shift;           // log2(G / 64)
   int ksplit;
   int steps_per_split;
+  int strips;                // column strips (grid x); the staged kernels take strips of
+                             // N / strips (16..32) columns, the register kernel N / 32
 };
 
 hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,

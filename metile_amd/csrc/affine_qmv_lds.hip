@@ -45,7 +45,9 @@ __device__ __forceinline__ uint16_t quiet_nan() {
   return DT == kBF16 ? (uint16_t)0x7FC0u : (uint16_t)0x7E00u;
 }
 
-// One workgroup's share: output strip `strip` (32 columns) over K split `split`.
+// One workgroup's share: output strip `strip` (columns [strip N / strips, (strip + 1) N /
+// strips), at most 32) over K split `split`. Lanes and rows past the strip's width load
+// nothing and store nothing.
 template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE>
 __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, const int split,
                                          unsigned char* __restrict__ dyn, int& flag,
@@ -63,6 +65,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const int j = lane & 31;
   const int h = lane >> 5;
   const int M = p.M, K = p.K, N = p.N;
+  const int col0 = (int)(((int64_t)strip * N) / p.strips);
+  const int width = (int)(((int64_t)(strip + 1) * N) / p.strips) - col0;
   const int steps_total = K >> 6;
   const int s_beg = split * p.steps_per_split;
   const int s_end = min(steps_total, s_beg + p.steps_per_split);
@@ -98,11 +102,11 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   for (int a = 0; a < kArrays; ++a) {
     const uint16_t* src = (a & 1) ? p.b[a >> 1] : p.s[a >> 1];
     const __amdgpu_buffer_rsrc_t r = make_rsrc(src, (uint32_t)N * groups_per_row * 2u);
-    const uint32_t base = (((uint32_t)(strip * 32 + sb_row) * groups_per_row + g_beg) * 2u) & ~3u;
+    const uint32_t base = (((uint32_t)(col0 + sb_row) * groups_per_row + g_beg) * 2u) & ~3u;
 #pragma unroll
     for (int k = 0; k < kSbIters; ++k) {
       const int q = sb_q0 + k * (kThreads / 32);
-      sbv[a][k] = load16(r, 4 * q < nwords ? base + 16u * q : kOOB);
+      sbv[a][k] = load16(r, (4 * q < nwords && sb_row < width) ? base + 16u * q : kOOB);
     }
   }
 
@@ -125,12 +129,13 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   if constexpr (ROLE != kDown) issue_x();
 
   // ---- code ring ---------------------------------------------------------------------------
-  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + (uint32_t)h * 4u * BITS;
+  const uint32_t w_row =
+      j < width ? (uint32_t)(col0 + j) * row_bytes + (uint32_t)h * 4u * BITS : kOOB;
   typedef u32x4 StageW[NPROJ][BITS / 4];
   StageW ring[STAGES];
   auto load_stage = [&](StageW& S, int st) {
     const bool ok = st < w_end;
-    const uint32_t woff = ok ? w_row + (uint32_t)st * 8u * BITS : kOOB;
+    const uint32_t woff = (ok && w_row != kOOB) ? w_row + (uint32_t)st * 8u * BITS : kOOB;
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
@@ -216,7 +221,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const f32x16 zero16 = (f32x16){0};
   const PairedConsts pc = paired_consts<DT>();
   const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(sb);
-  const int sb_shift = ((strip * 32 + j) * groups_per_row + g_beg) & 1;
+  const int sb_shift = ((col0 + j) * groups_per_row + g_beg) & 1;
   // A operand of lane (j, h): row j (the zero row for j >= M), elements [32 h, 32 h + 32) of
   // each step's 64.
   const uint32_t a_base = lay.x + ((uint32_t)min(j, M) * xstride + 32u * h) * 2u;
@@ -285,7 +290,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)M * N * 2u);
   // Final value of output (i, c) of this strip from its K sums v[].
   auto finish = [&](int i, int c, const float (&v)[NPROJ]) {
-    const size_t oi = (size_t)i * N + strip * 32 + c;
+    const size_t oi = (size_t)i * N + col0 + c;
     float out;
     if constexpr (NPROJ == 2) {
       out = silu_mul(v[0], v[1]);
@@ -329,6 +334,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const int outs = M * 32;
   if (p.ksplit == 1) {
     for (int o = tid; o < outs; o += kThreads) {
+      if ((o & 31) >= width) continue;
       float v[NPROJ];
 #pragma unroll
       for (int pr = 0; pr < NPROJ; ++pr) v[pr] = reduce(pr, o >> 5, o & 31);
@@ -347,10 +353,11 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const size_t plane = (size_t)M * N;
   for (int o = tid; o < outs; o += kThreads) {
     const int i = o >> 5, c = o & 31;
+    if (c >= width) continue;
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
       __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + pr) * plane + (size_t)i * N +
-                                    strip * 32 + c],
+                                    col0 + c],
                          reduce(pr, i, c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -367,7 +374,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   }
   for (int o = tid; o < outs; o += kThreads) {
     const int i = o >> 5, c = o & 31;
-    const size_t oi = (size_t)i * N + strip * 32 + c;
+    if (c >= width) continue;
+    const size_t oi = (size_t)i * N + col0 + c;
     float v[NPROJ];
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr) {
@@ -406,12 +414,12 @@ void affine_mlp_kernel(const QmvParams up, const QmvParams down, const MlpLink l
   constexpr int kStagesDown = BITS == 4 ? 6 : 4;
   const int id = blockIdx.x;
   if (id < blocks_up) {
-    const int strips = up.N / 32;
+    const int strips = up.strips;
     lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp>(up, id % strips,
                                                                       id / strips, dyn_mlp, flag,
                                                                       link);
   } else {
-    const int strips = down.N / 32;
+    const int strips = down.strips;
     const int idd = id - blocks_up;
     lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown>(down, idd % strips,
                                                                   idd / strips, dyn_mlp, flag,
@@ -430,7 +438,7 @@ template <int BITS, int DT, int MROWS, int NPROJ>
 hipError_t launch_lds_rows(const QmvParams& p, hipStream_t stream) {
   constexpr int kStages = BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4);
   const QmvLdsLayout lay = qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ);
-  const dim3 grid(p.N / 32, p.ksplit);
+  const dim3 grid(p.strips, p.ksplit);
   auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages>;
   static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
   if (attr != hipSuccess) return attr;
@@ -455,7 +463,7 @@ hipError_t launch_mlp_rows(const QmvParams& up, const QmvParams& down, const Mlp
                            hipStream_t stream) {
   const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2);
   const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1);
-  const int blocks_up = (up.N / 32) * up.ksplit;
+  const int blocks_up = up.strips * up.ksplit;
   const int blocks = blocks_up + link.down_blocks;
   auto kernel = affine_mlp_kernel<BITS, DT, MROWS>;
   static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));

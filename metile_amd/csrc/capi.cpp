@@ -37,15 +37,17 @@ constexpr int kRowChunk = 32;  // rows per small-row dispatch
 constexpr size_t kCounterBytes = 64 * 1024;
 constexpr int kMaxStrips = (int)(kCounterBytes / 4);
 
-// Split-K plan of the small-row kernel for one (K, N): about one workgroup per CU (splitting
+// Split-K plan of the streaming kernels for one (K, N): about one workgroup per CU (splitting
 // further costs more in partial-sum traffic and reduction than it gains in parallelism), with
-// at least 16 K steps in each split. Depends only on K and N.
+// at least 16 K steps in each split. Depends only on K and N. `strips` = N / 32.
 struct Plan {
   int ksplit;
   int steps_per_split;
+  int strips;
+  bool staged;  // activation-staged small-row kernel
 };
 
-Plan plan_qmv(int K, int N) {
+Plan plan_split(int K, int N) {
   const int steps = K / 64;
   const int strips = N / 32;
   int ksplit = (256 + strips / 2) / strips;
@@ -62,6 +64,8 @@ Plan plan_qmv(int K, int N) {
   Plan p;
   p.steps_per_split = (steps + ksplit - 1) / ksplit;
   p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
+  p.strips = strips;
+  p.staged = false;
   return p;
 }
 
@@ -73,11 +77,52 @@ bool use_lds_path(int rows, int steps_per_split, int nproj) {
   return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj);
 }
 
+constexpr int kCus = 256;  // compute units of an MI355X
+
+// Plan of one small-row call chunk of `rows` rows: the split plan, and for the staged kernel
+// a strip count that evens out the CUs. Its column strips need not be 32 wide: a workgroup
+// takes columns [s N / strips, (s + 1) N / strips) (16 to 32 of them; the MFMA tile masks
+// the rest). When the grid of 32-column strips is not a whole number of workgroups per CU,
+// take the smallest strip count that is, if it lowers the columns the busiest CU streams:
+// with N / 32 = 280 strips on 256 CUs, 24 CUs would otherwise stream two full strips and set
+// the kernel's time. Only grids that are resident at once (two eight-wave workgroups per CU)
+// are rebalanced: a grid of several rounds evens out as workgroups retire, and its narrower
+// strips measured slower. (Changing the K split instead also measured slower: every split
+// adds a partial-sum hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
+Plan plan_qmv(int rows, int K, int N, int nproj) {
+  Plan plan = plan_split(K, N);
+  if (!use_lds_path(rows, plan.steps_per_split, nproj)) return plan;
+  plan.staged = true;
+  const char* env = std::getenv("METILE_AMD_STRIPS");
+  if (env && std::string(env) == "32") return plan;
+  const long base = N / 32, ks = plan.ksplit;
+  const long per_cu_base = (base * ks + kCus - 1) / kCus;  // workgroups on the busiest CU
+  for (long rounds = per_cu_base; rounds <= per_cu_base + 1; ++rounds) {
+    if ((rounds * kCus) % ks) continue;
+    const long strips = rounds * kCus / ks;
+    if (strips <= base || strips > 2 * base || strips > kMaxStrips) continue;
+    if (strips * ks > 2L * kCus) break;
+    // Columns the busiest CU streams: rounds strips of N / strips columns against
+    // per_cu_base strips of 32.
+    if (rounds * N < per_cu_base * 32 * strips) {
+      plan.strips = (int)strips;
+      break;
+    }
+  }
+  return plan;
+}
+
 size_t qmv_workspace(int M, int K, int N, int nproj) {
-  const Plan plan = plan_qmv(K, N);
-  if (plan.ksplit <= 1) return 0;
-  const int rows = M < kRowChunk ? M : kRowChunk;
-  return kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+  // Row chunks of kRowChunk rows and one remainder chunk may plan differently.
+  size_t need = 0;
+  for (int rows : {M < kRowChunk ? M : kRowChunk, M % kRowChunk}) {
+    if (rows < 1) continue;
+    const Plan plan = plan_qmv(rows, K, N, nproj);
+    if (plan.ksplit <= 1) continue;
+    const size_t b = kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+    if (b > need) need = b;
+  }
+  return need;
 }
 
 int check_affine(const char* op, int M, int K, int N, int group_size, int bits, int dtype) {
@@ -118,10 +163,10 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
-  const Plan plan = plan_qmv(K, N);
   const hipStream_t hs = static_cast<hipStream_t>(stream);
   for (int r0 = 0; r0 < M; r0 += kRowChunk) {
     const int rows = (M - r0) < kRowChunk ? (M - r0) : kRowChunk;
+    const Plan plan = plan_qmv(rows, K, N, nproj);
     mt::QmvParams p{};
     p.x = static_cast<const uint16_t*>(x) + (size_t)r0 * K;
     for (int q = 0; q < nproj; ++q) {
@@ -142,9 +187,9 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.group_shift = __builtin_ctz((unsigned)(group_size / 64));
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
-    const hipError_t e = use_lds_path(rows, plan.steps_per_split, nproj)
-                             ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
-                             : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
+    p.strips = plan.strips;
+    const hipError_t e = plan.staged ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
+                                     : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
     if (e != hipSuccess) return hip_fail(e, op);
   }
   return MT_OK;
@@ -153,7 +198,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
 constexpr int kDenseRowChunk = 128;  // rows per dense dispatch
 
 size_t dense_workspace(int M, int K, int N, int nproj) {
-  const Plan plan = plan_qmv(K, N);
+  const Plan plan = plan_split(K, N);
   if (plan.ksplit <= 1) return 0;
   const int rows = M < kDenseRowChunk ? M : kDenseRowChunk;
   return kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
@@ -187,7 +232,7 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
-  const Plan plan = plan_qmv(K, N);
+  const Plan plan = plan_split(K, N);
   for (int r0 = 0; r0 < M; r0 += kDenseRowChunk) {
     const int rows = (M - r0) < kDenseRowChunk ? (M - r0) : kDenseRowChunk;
     mt::DenseParams p{};
@@ -264,8 +309,8 @@ struct MlpPlan {
 
 MlpPlan plan_mlp(int M, int H, int I) {
   MlpPlan mp{};
-  mp.up = plan_qmv(H, I);
-  mp.down = plan_qmv(I, H);
+  mp.up = plan_split(H, I);
+  mp.down = plan_split(I, H);
   // The one-launch MLP is opt-in (METILE_AMD_MLP_PATH=fused): on MI355X its hand-off chain
   // (hidden-strip store acknowledgement, counter, coherent reload) costs several HBM round
   // trips while the weight stream is still in flight, which measured slower than two launches.
@@ -396,6 +441,7 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   up.N = I;
   up.ksplit = mp.up.ksplit;
   up.steps_per_split = mp.up.steps_per_split;
+  up.strips = strips_up;
   down.x = static_cast<const uint16_t*>(h);
   down.w[0] = down_w;
   down.s[0] = static_cast<const uint16_t*>(down_scales);
@@ -409,6 +455,7 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   down.N = H;
   down.ksplit = mp.down.ksplit;
   down.steps_per_split = mp.down.steps_per_split;
+  down.strips = strips_down;
   up.G = down.G = group_size;
   up.group_shift = down.group_shift = __builtin_ctz((unsigned)(group_size / 64));
   mt::MlpLink link{};
