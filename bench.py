@@ -274,6 +274,17 @@ def traffic_probe(mt, gen, device, args):
     print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20}), flush=True)
 
 
+def prefill_probe(mt, gen, device):
+    """Eager launches for the prefill GEMM counter runs: three of each config-4 projection."""
+    for k, n in ((HIDDEN, INTER), (INTER, HIDDEN)):
+        w = make_affine(gen, device, k, n)
+        x = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
+        for _ in range(3):
+            mt.affine_matmul(x, *w, group_size=GROUP, bits=BITS)
+        torch.cuda.synchronize()
+    print(json.dumps({"prefill_probe": "done"}), flush=True)
+
+
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "affine_qmv_lds_swiglu_m1_hbm_traffic.md")
 
@@ -339,6 +350,8 @@ def main():
                     help="comma-separated row counts of the headline MLP (default: all)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the eager launches profiled by the HBM-traffic counter runs")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only eager config-4 GEMM launches, for instruction-counter runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the hot path runs on a single MI355X and this "
@@ -354,6 +367,9 @@ def main():
     stream = torch.cuda.Stream(device)
     if args.traffic_probe:
         traffic_probe(mt, gen, device, args)
+        return
+    if args.prefill_probe:
+        prefill_probe(mt, gen, device)
         return
 
     with torch.cuda.stream(stream):

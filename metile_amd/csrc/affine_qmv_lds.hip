@@ -110,6 +110,16 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
     }
   }
 
+  // ---- the residual this thread's output (row tid / 32, column tid % 32) adds, requested now
+  // so that the workgroup finishing the strip does not wait for it at the end --------------
+  static_assert(MROWS * 32 <= kThreads, "one output per thread in the epilogue");
+  uint16_t res_pre = 0;
+  if constexpr (NPROJ == 1) {
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.residual, p.residual ? (uint32_t)M * N * 2u : 0u);
+    const int ri = tid >> 5, rc = tid & 31;
+    res_pre = load2(rr, (ri < M && rc < width) ? ((uint32_t)ri * N + col0 + rc) * 2u : kOOB);
+  }
+
   // ---- activation chunks: chunk c = row * cpr + cc holds elements [8 cc, 8 cc + 8) --------
   const int cpr = steps_here * 8;
   const int nchunks = M * cpr;
@@ -296,7 +306,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
       out = silu_mul(v[0], v[1]);
     } else {
       out = v[0];
-      if (p.residual) out += act_to_f32<DT>(p.residual[oi]);
+      if (p.residual) out += act_to_f32<DT>(res_pre);  // output i * 32 + c is this thread's
     }
     const uint16_t o16 = timed_out ? quiet_nan<DT>() : f32_to_act<DT>(out);
     if constexpr (ROLE == kGateUp) {
