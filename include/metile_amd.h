@@ -51,8 +51,9 @@ size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bi
 /* y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/G] + b[n, k/G]) (+ residual[m, n]).
  * Replaces mlx_affine_qmv (metile/backends/mlx_quantized.py:691-714) and, with a residual,
  * mlx_affine_residual_qmv (metile/backends/mlx_quantized.py:1538-1624); the kernels they
- * bind are kernels/affine_qmv.py:57-132. bits in {4, 8}; group_size a multiple of 64 that
- * divides K; K % 64 == 0; N % 32 == 0; any M >= 1 (rows beyond 32 run in 32-row chunks). */
+ * bind are kernels/affine_qmv.py:57-132. bits in {4, 8}; group_size a power of two >= 32
+ * that divides K; K % 64 == 0; N % 32 == 0; any M >= 1 (rows beyond 32 run in 32-row
+ * chunks, 16-row chunks for groups of 32). */
 int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
                   const void* residual, void* y, int M, int K, int N, int group_size, int bits,
                   int dtype, void* workspace, size_t workspace_bytes, void* stream);

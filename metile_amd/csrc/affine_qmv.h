@@ -46,7 +46,8 @@ __host__ __device__ constexpr int qmv_lds_chunk_iters(int mrows) { return mrows 
 // Dynamic LDS of one workgroup, byte offsets: scales and biases [2 nproj][32][kSbRowWords]
 // (32-bit words), activation rows [M + 1][steps_per_split * 64 + 8] (16-bit; row M is all
 // zeros and stands in for rows M..31 of the MFMA tile), per-step row sums
-// [steps_per_split][mrows] (fp32). After the K loop the cross-wave reduction buffer
+// [steps_per_split * halves][mrows] (fp32; halves = 2 for groups of 32, one sum per group).
+// After the K loop the cross-wave reduction buffer
 // [waves][nproj][mrows][33] (fp32) reuses the space from offset 0.
 struct QmvLdsLayout {
   uint32_t x;
@@ -56,21 +57,22 @@ struct QmvLdsLayout {
 };
 
 __host__ __device__ inline QmvLdsLayout qmv_lds_layout(int M, int steps_per_split, int mrows,
-                                                       int nproj) {
+                                                       int nproj, int halves) {
   QmvLdsLayout l;
   const uint32_t row = (uint32_t)(steps_per_split * 64 + 8) * 2u;
   l.x = (uint32_t)(2 * nproj * 32 * kSbRowWords) * 4u;
   l.zero = l.x + (uint32_t)M * row;
   l.xsum = l.zero + row;
-  const uint32_t staged = l.xsum + (uint32_t)(steps_per_split * mrows) * 4u;
+  const uint32_t staged = l.xsum + (uint32_t)(steps_per_split * halves * mrows) * 4u;
   const uint32_t red = (uint32_t)(kQmvLdsWaves * nproj * mrows * 33) * 4u;
   l.bytes = staged > red ? staged : red;
   return l;
 }
 
 // Whether the activation-staged kernels take M rows split into K ranges of steps_per_split
-// 64-wide steps (the staging must fit the per-thread chunk budget and kQmvLdsMaxBytes).
-bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj);
+// 64-wide steps (the staging must fit the per-thread chunk budget, the scale rows and
+// kQmvLdsMaxBytes). They are the only small-row kernels for groups of 32.
+bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size);
 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,
                                  hipStream_t stream);

@@ -48,7 +48,10 @@ __device__ __forceinline__ uint16_t quiet_nan() {
 // One workgroup's share: output strip `strip` (columns [strip N / strips, (strip + 1) N /
 // strips), at most 32) over K split `split`. Lanes and rows past the strip's width load
 // nothing and store nothing.
-template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE>
+// HALF: groups of 32, two per 64-wide K step. Each projection then runs two MFMA chains per
+// step, one per group: lanes of the other K half (h) read the zero row, so each chain sums one
+// group only and gets its own scale, bias and row sum.
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE, bool HALF>
 __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, const int split,
                                          unsigned char* __restrict__ dyn, int& flag,
                                          const MlpLink& link) {
@@ -58,6 +61,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   constexpr int kRegs = MROWS / 2;
   constexpr int kArrays = 2 * NPROJ;
   constexpr int kXIters = qmv_lds_chunk_iters(MROWS);
+  constexpr int kHalves = HALF ? 2 : 1;  // row sums (groups) per K step
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -77,13 +81,13 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const int gshift = p.group_shift;
   // Scale rows are staged from the 32-bit word holding group g_beg; a row whose element
   // index (row * groups_per_row + g_beg) is odd starts one 16-bit element into its segment.
-  const int g_beg = s_beg >> gshift;
-  const int g_last = (s_end - 1) >> gshift;
+  const int g_beg = HALF ? 2 * s_beg : s_beg >> gshift;
+  const int g_last = HALF ? 2 * s_end - 1 : (s_end - 1) >> gshift;
   const int nwords = (g_last - g_beg + 1) / 2 + 1;
-  const QmvLdsLayout lay = qmv_lds_layout(M, p.steps_per_split, MROWS, NPROJ);
+  const QmvLdsLayout lay = qmv_lds_layout(M, p.steps_per_split, MROWS, NPROJ, kHalves);
   const int xstride = p.steps_per_split * 64 + 8;  // staged row stride, elements
   uint32_t* sb = reinterpret_cast<uint32_t*>(dyn);  // [kArrays][32][kSbRowWords]
-  float* xsum = reinterpret_cast<float*>(dyn + lay.xsum);  // [steps_per_split][MROWS]
+  float* xsum = reinterpret_cast<float*>(dyn + lay.xsum);  // [steps_per_split * kHalves][MROWS]
 
   const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
   const int groups_per_row = K / p.G;
@@ -201,19 +205,21 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
     if (i * kThreads < nchunks) {
       const int row = (int)(((float)c + 0.5f) * inv_cpr);
       const int cc = c - row * cpr;
+      // Sum over the chunks of one group: 8 (a whole step) or 4 (a half step).
       float s = sum8<DT>(xv[i], 0.0f);
       s += __shfl_xor(s, 1);
       s += __shfl_xor(s, 2);
-      s += __shfl_xor(s, 4);
+      if constexpr (!HALF) s += __shfl_xor(s, 4);
       if (c < nchunks) {
         const u32x4 v = (BITS == 4) ? pair_order(xv[i]) : xv[i];
         *reinterpret_cast<u32x4*>(dyn + lay.x + ((uint32_t)row * xstride + cc * 8) * 2u) = v;
-        if ((cc & 7) == 0) xsum[(cc >> 3) * MROWS + row] = s;
+        constexpr int kChunksPerSum = HALF ? 4 : 8;
+        if ((cc & (kChunksPerSum - 1)) == 0) xsum[(cc / kChunksPerSum) * MROWS + row] = s;
       }
     }
   }
   // Row sums of rows M..MROWS-1 and the zero row.
-  for (int idx = tid; idx < steps_here * MROWS; idx += kThreads)
+  for (int idx = tid; idx < steps_here * kHalves * MROWS; idx += kThreads)
     if ((idx % MROWS) >= M) xsum[idx] = 0.0f;
   for (int q = tid; q < xstride / 8; q += kThreads)
     *reinterpret_cast<u32x4*>(dyn + lay.zero + 16u * q) = (u32x4){0u, 0u, 0u, 0u};
@@ -235,6 +241,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   // A operand of lane (j, h): row j (the zero row for j >= M), elements [32 h, 32 h + 32) of
   // each step's 64.
   const uint32_t a_base = lay.x + ((uint32_t)min(j, M) * xstride + 32u * h) * 2u;
+  const uint32_t z_base = lay.x + ((uint32_t)M * xstride + 32u * h) * 2u;
   for (int s0 = w_beg; s0 < w_end; s0 += STAGES) {
 #pragma unroll
     for (int d = 0; d < STAGES; ++d) {
@@ -242,37 +249,50 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
       const int st = s0 + d;
       if (st < w_end) {
         const int sl = st - s_beg;
-        const unsigned char* ap = dyn + a_base + (uint32_t)sl * 128u;
-        u32x4 a[4];
+        // A operands of each chain: chain g takes the real row in lanes of K half h == g (all
+        // lanes when the step is one group) and the zero row elsewhere.
+        u32x4 a[kHalves][4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a[e] = *reinterpret_cast<const u32x4*>(ap + 16 * e);
-        float xs[kRegs];
+        for (int g = 0; g < kHalves; ++g) {
+          const uint32_t base = (!HALF || h == g) ? a_base : z_base;
+          const unsigned char* ap = dyn + base + (uint32_t)sl * 128u;
 #pragma unroll
-        for (int q = 0; q < kRegs / 4; ++q) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(&xsum[sl * MROWS + 8 * q + 4 * h]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xs[4 * q + r] = v[r];
+          for (int e = 0; e < 4; ++e) a[g][e] = *reinterpret_cast<const u32x4*>(ap + 16 * e);
         }
-        const int gl = (st >> gshift) - g_beg + sb_shift;
+        float xs[kHalves][kRegs];
+#pragma unroll
+        for (int g = 0; g < kHalves; ++g)
+#pragma unroll
+          for (int q = 0; q < kRegs / 4; ++q) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(
+                &xsum[(sl * kHalves + g) * MROWS + 8 * q + 4 * h]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) xs[g][4 * q + r] = v[r];
+          }
+        const int gl = (HALF ? 2 * st : (st >> gshift)) - g_beg + sb_shift;
 #pragma unroll
         for (int pr = 0; pr < NPROJ; ++pr) {
-          f32x16 t;
-          if constexpr (BITS == 4) {
-            t = mfma32<DT>(a[0], unpack_u4_paired(S[pr][0][0], pc), zero16);
+          u32x4 b[4];
 #pragma unroll
-            for (int e = 1; e < 4; ++e) t = mfma32<DT>(a[e], unpack_u4_paired(S[pr][0][e], pc), t);
-          } else {
-            t = mfma32<DT>(a[0], code_frag<BITS, DT>(S[pr], 0), zero16);
-#pragma unroll
-            for (int e = 1; e < 4; ++e) t = mfma32<DT>(a[e], code_frag<BITS, DT>(S[pr], e), t);
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (BITS == 4) b[e] = unpack_u4_paired(S[pr][0][e], pc);
+            else b[e] = code_frag<BITS, DT>(S[pr], e);
           }
-          const float sf = act_to_f32<DT>(sb16[((2 * pr) * 32 + j) * 2 * kSbRowWords + gl]);
-          const float bf = act_to_f32<DT>(sb16[((2 * pr + 1) * 32 + j) * 2 * kSbRowWords + gl]);
-          const float bp = __builtin_fmaf(-kOff, sf, bf);
 #pragma unroll
-          for (int r = 0; r < kRegs; ++r) {
-            acc[pr][r] = __builtin_fmaf(sf, t[r], acc[pr][r]);
-            acc[pr][r] = __builtin_fmaf(bp, xs[r], acc[pr][r]);
+          for (int g = 0; g < kHalves; ++g) {
+            f32x16 t = mfma32<DT>(a[g][0], b[0], zero16);
+#pragma unroll
+            for (int e = 1; e < 4; ++e) t = mfma32<DT>(a[g][e], b[e], t);
+            const int gg = gl + g;
+            const float sf = act_to_f32<DT>(sb16[((2 * pr) * 32 + j) * 2 * kSbRowWords + gg]);
+            const float bf =
+                act_to_f32<DT>(sb16[((2 * pr + 1) * 32 + j) * 2 * kSbRowWords + gg]);
+            const float bp = __builtin_fmaf(-kOff, sf, bf);
+#pragma unroll
+            for (int r = 0; r < kRegs; ++r) {
+              acc[pr][r] = __builtin_fmaf(sf, t[r], acc[pr][r]);
+              acc[pr][r] = __builtin_fmaf(bp, xs[g][r], acc[pr][r]);
+            }
           }
         }
       }
@@ -404,14 +424,14 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
 }
 
 // At most 128 registers, so that two eight-wave workgroups share a CU.
-template <int BITS, int DT, int MROWS, int NPROJ, int STAGES>
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, bool HALF>
 __global__ __launch_bounds__(kQmvLdsWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
 void affine_qmv_lds_kernel(const QmvParams p) {
   extern __shared__ __align__(16) unsigned char dyn_plain[];
   __shared__ int flag;
   const MlpLink none{};
-  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain>(p, blockIdx.x, blockIdx.y,
-                                                                   dyn_plain, flag, none);
+  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain, HALF>(
+      p, blockIdx.x, blockIdx.y, dyn_plain, flag, none);
 }
 
 template <int BITS, int DT, int MROWS>
@@ -425,13 +445,13 @@ void affine_mlp_kernel(const QmvParams up, const QmvParams down, const MlpLink l
   const int id = blockIdx.x;
   if (id < blocks_up) {
     const int strips = up.strips;
-    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp>(up, id % strips,
+    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp, false>(up, id % strips,
                                                                       id / strips, dyn_mlp, flag,
                                                                       link);
   } else {
     const int strips = down.strips;
     const int idd = id - blocks_up;
-    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown>(down, idd % strips,
+    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown, false>(down, idd % strips,
                                                                   idd / strips, dyn_mlp, flag,
                                                                   link);
   }
@@ -444,22 +464,29 @@ hipError_t allow_lds(const void* kernel) {
                              (int)kQmvLdsMaxBytes);
 }
 
-template <int BITS, int DT, int MROWS, int NPROJ>
+template <int BITS, int DT, int MROWS, int NPROJ, bool HALF>
 hipError_t launch_lds_rows(const QmvParams& p, hipStream_t stream) {
-  constexpr int kStages = BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4);
-  const QmvLdsLayout lay = qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ);
+  // Groups of 32 hold two A operand sets per step, so their ring is shallower.
+  constexpr int kStages = HALF ? (BITS == 4 ? 3 : 2) : (BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4));
+  const QmvLdsLayout lay = qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ, HALF ? 2 : 1);
   const dim3 grid(p.strips, p.ksplit);
-  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages>;
+  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages, HALF>;
   static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
   if (attr != hipSuccess) return attr;
   kernel<<<grid, dim3(kQmvLdsWaves * 64), lay.bytes, stream>>>(p);
   return hipGetLastError();
 }
 
+template <int BITS, int DT, int NPROJ, bool HALF>
+hipError_t launch_lds_half(const QmvParams& p, hipStream_t stream) {
+  return p.M <= 8 ? launch_lds_rows<BITS, DT, 8, NPROJ, HALF>(p, stream)
+                  : launch_lds_rows<BITS, DT, 16, NPROJ, HALF>(p, stream);
+}
+
 template <int BITS, int DT, int NPROJ>
 hipError_t launch_lds_nproj(const QmvParams& p, hipStream_t stream) {
-  return p.M <= 8 ? launch_lds_rows<BITS, DT, 8, NPROJ>(p, stream)
-                  : launch_lds_rows<BITS, DT, 16, NPROJ>(p, stream);
+  return p.G == 32 ? launch_lds_half<BITS, DT, NPROJ, true>(p, stream)
+                   : launch_lds_half<BITS, DT, NPROJ, false>(p, stream);
 }
 
 template <int BITS, int DT>
@@ -471,8 +498,8 @@ hipError_t launch_lds_bits_dt(const QmvParams& p, int nproj, hipStream_t stream)
 template <int BITS, int DT, int MROWS>
 hipError_t launch_mlp_rows(const QmvParams& up, const QmvParams& down, const MlpLink& link,
                            hipStream_t stream) {
-  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2);
-  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1);
+  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2, 1);
+  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1, 1);
   const int blocks_up = up.strips * up.ksplit;
   const int blocks = blocks_up + link.down_blocks;
   auto kernel = affine_mlp_kernel<BITS, DT, MROWS>;
@@ -492,11 +519,15 @@ hipError_t launch_mlp_bits_dt(const QmvParams& up, const QmvParams& down, const 
 
 }  // namespace
 
-bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj) {
+bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size) {
   if (M < 1 || M > kQmvLdsMaxRows) return false;
   const int mrows = M <= 8 ? 8 : 16;
   if (M * steps_per_split * 8 > qmv_lds_chunk_iters(mrows) * kQmvLdsWaves * 64) return false;
-  return qmv_lds_layout(M, steps_per_split, mrows, nproj).bytes <= kQmvLdsMaxBytes;
+  // Groups staged per split (one more may straddle) within the scale rows.
+  const int groups = group_size == 32 ? 2 * steps_per_split : steps_per_split;
+  if (groups > kMaxGroupsPerSplit - 1) return false;
+  const int halves = group_size == 32 ? 2 : 1;
+  return qmv_lds_layout(M, steps_per_split, mrows, nproj, halves).bytes <= kQmvLdsMaxBytes;
 }
 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,

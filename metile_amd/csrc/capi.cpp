@@ -70,11 +70,12 @@ Plan plan_split(int K, int N) {
 }
 
 // Activation-staged small-row kernel where it fits (M <= 16 and a bounded K range per
-// split); METILE_AMD_QMV_PATH=reg forces the register-staged kernel (for comparisons).
-bool use_lds_path(int rows, int steps_per_split, int nproj) {
+// split); METILE_AMD_QMV_PATH=reg forces the register-staged kernel (for comparisons) except
+// for groups of 32, which only the staged kernel handles.
+bool use_lds_path(int rows, int steps_per_split, int nproj, int group_size) {
   const char* env = std::getenv("METILE_AMD_QMV_PATH");
-  if (env && std::string(env) == "reg") return false;
-  return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj);
+  if (group_size != 32 && env && std::string(env) == "reg") return false;
+  return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size);
 }
 
 constexpr int kCus = 256;  // compute units of an MI355X
@@ -89,9 +90,22 @@ constexpr int kCus = 256;  // compute units of an MI355X
 // are rebalanced: a grid of several rounds evens out as workgroups retire, and its narrower
 // strips measured slower. (Changing the K split instead also measured slower: every split
 // adds a partial-sum hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
-Plan plan_qmv(int rows, int K, int N, int nproj) {
+Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
   Plan plan = plan_split(K, N);
-  if (!use_lds_path(rows, plan.steps_per_split, nproj)) return plan;
+  if (group_size == 32) {
+    // Two groups per K step: split K until the staged kernel's scale rows and LDS take it.
+    const int steps = K / 64;
+    for (int ks = plan.ksplit; ks <= steps; ++ks) {
+      Plan c = plan;
+      c.steps_per_split = (steps + ks - 1) / ks;
+      c.ksplit = (steps + c.steps_per_split - 1) / c.steps_per_split;
+      if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size)) {
+        plan = c;
+        break;
+      }
+    }
+  }
+  if (!use_lds_path(rows, plan.steps_per_split, nproj, group_size)) return plan;
   plan.staged = true;
   const char* env = std::getenv("METILE_AMD_STRIPS");
   if (env && std::string(env) == "32") return plan;
@@ -112,12 +126,17 @@ Plan plan_qmv(int rows, int K, int N, int nproj) {
   return plan;
 }
 
-size_t qmv_workspace(int M, int K, int N, int nproj) {
-  // Row chunks of kRowChunk rows and one remainder chunk may plan differently.
+// Rows per small-row dispatch: 32 (the register kernel's tile), 16 for groups of 32 (the
+// staged kernel's largest row bucket).
+int row_chunk(int group_size) { return group_size == 32 ? mt::kQmvLdsMaxRows : kRowChunk; }
+
+size_t qmv_workspace(int M, int K, int N, int nproj, int group_size) {
+  // Row chunks and one remainder chunk may plan differently.
+  const int chunk = row_chunk(group_size);
   size_t need = 0;
-  for (int rows : {M < kRowChunk ? M : kRowChunk, M % kRowChunk}) {
+  for (int rows : {M < chunk ? M : chunk, M % chunk}) {
     if (rows < 1) continue;
-    const Plan plan = plan_qmv(rows, K, N, nproj);
+    const Plan plan = plan_qmv(rows, K, N, nproj, group_size);
     if (plan.ksplit <= 1) continue;
     const size_t b = kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
     if (b > need) need = b;
@@ -132,9 +151,9 @@ int check_affine(const char* op, int M, int K, int N, int group_size, int bits, 
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": dtype must be MT_BF16 or MT_F16");
   if (M < 1 || K < 1 || N < 1)
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": M, K and N must be positive");
-  if (group_size < 64 || (group_size & (group_size - 1)) || K % group_size)
+  if (group_size < 32 || (group_size & (group_size - 1)) || K % group_size)
     return fail(MT_ERR_INVALID_ARGUMENT,
-                std::string(op) + ": group_size must be a power of two >= 64 that divides K");
+                std::string(op) + ": group_size must be a power of two >= 32 that divides K");
   if (K % 64 || N % 32)
     return fail(MT_ERR_INVALID_ARGUMENT,
                 std::string(op) + ": K must be a multiple of 64 and N a multiple of 32");
@@ -159,14 +178,18 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     if (!w[q] || !s[q] || !b[q])
       return fail(MT_ERR_INVALID_ARGUMENT,
                   std::string(op) + ": null packed weight, scales or biases");
-  const size_t need = qmv_workspace(M, K, N, nproj);
+  const size_t need = qmv_workspace(M, K, N, nproj, group_size);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
   const hipStream_t hs = static_cast<hipStream_t>(stream);
-  for (int r0 = 0; r0 < M; r0 += kRowChunk) {
-    const int rows = (M - r0) < kRowChunk ? (M - r0) : kRowChunk;
-    const Plan plan = plan_qmv(rows, K, N, nproj);
+  const int chunk = row_chunk(group_size);
+  for (int r0 = 0; r0 < M; r0 += chunk) {
+    const int rows = (M - r0) < chunk ? (M - r0) : chunk;
+    const Plan plan = plan_qmv(rows, K, N, nproj, group_size);
+    if (group_size == 32 && !plan.staged)
+      return fail(MT_ERR_INVALID_ARGUMENT,
+                  std::string(op) + ": no staged plan fits groups of 32 at this shape");
     mt::QmvParams p{};
     p.x = static_cast<const uint16_t*>(x) + (size_t)r0 * K;
     for (int q = 0; q < nproj; ++q) {
@@ -184,7 +207,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.K = K;
     p.N = N;
     p.G = group_size;
-    p.group_shift = __builtin_ctz((unsigned)(group_size / 64));
+    p.group_shift = group_size >= 64 ? __builtin_ctz((unsigned)(group_size / 64)) : 0;
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
     p.strips = plan.strips;
@@ -307,7 +330,7 @@ struct MlpPlan {
   size_t up_partial, down_partial, hidden, bytes;  // workspace offsets (bytes) and total
 };
 
-MlpPlan plan_mlp(int M, int H, int I) {
+MlpPlan plan_mlp(int M, int H, int I, int group_size) {
   MlpPlan mp{};
   mp.up = plan_split(H, I);
   mp.down = plan_split(I, H);
@@ -327,10 +350,10 @@ MlpPlan plan_mlp(int M, int H, int I) {
   for (; ks <= steps_down; ++ks) {
     down.steps_per_split = (steps_down + ks - 1) / ks;
     down.ksplit = (steps_down + down.steps_per_split - 1) / down.steps_per_split;
-    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1)) break;
+    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1, 64)) break;
   }
   mp.fused = !forced_split && M <= mt::kQmvLdsMaxRows && ks <= steps_down &&
-             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2) &&
+             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2, 64) && group_size >= 64 &&
              strips_up + strips_down + down.ksplit + 1 <= kMaxStrips;
   if (mp.fused) {
     mp.down = down;
@@ -342,8 +365,8 @@ MlpPlan plan_mlp(int M, int H, int I) {
         mp.down.ksplit > 1 ? align_up((size_t)mp.down.ksplit * M * H * 4) : 0;
     mp.hidden = mp.down_partial + down_bytes;
   } else {
-    const size_t a = qmv_workspace(M, H, I, 2);
-    const size_t b = qmv_workspace(M, I, H, 1);
+    const size_t a = qmv_workspace(M, H, I, 2, group_size);
+    const size_t b = qmv_workspace(M, I, H, 1, group_size);
     const size_t split = align_up(a > b ? a : b);
     mp.hidden = split > kCounterBytes ? split : kCounterBytes;
   }
@@ -362,7 +385,7 @@ const char* mt_last_error(void) { return g_last_error.c_str(); }
 size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj) {
   if (check_affine("mt_affine_qmv_workspace_bytes", M, K, N, group_size, bits, MT_BF16))
     return 0;
-  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1);
+  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1, group_size);
 }
 
 int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
@@ -390,7 +413,7 @@ size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bi
   if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
       check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
     return 0;
-  return plan_mlp(M, H, I).bytes;
+  return plan_mlp(M, H, I, group_size).bytes;
 }
 
 int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
@@ -410,7 +433,7 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   if (!x || !y || !gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases ||
       !down_w || !down_scales || !down_biases)
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_mlp: null pointer");
-  const MlpPlan mp = plan_mlp(M, H, I);
+  const MlpPlan mp = plan_mlp(M, H, I, group_size);
   char* ws = static_cast<char*>(workspace);
   void* h = ws + mp.hidden;
   if (!mp.fused) {
@@ -513,7 +536,7 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
 
 size_t mt_affine_gemm_workspace_bytes(int M, int K, int N, int group_size, int bits) {
   if (check_affine("mt_affine_gemm_workspace_bytes", 1, K, N, group_size, bits, MT_BF16) ||
-      M < 1)
+      M < 1 || group_size < 64)
     return 0;
   return gemm_workspace(M, K, N);
 }
@@ -525,6 +548,9 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
   if (st) return st;
   if (bits != 4)
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: the prefill GEMM takes 4-bit codes");
+  if (group_size < 64)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "mt_affine_gemm: the prefill GEMM takes groups of 64 or more");
   if (M < 1) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: M must be positive");
   if ((size_t)M * K * 2 >= (1ull << 31) || (size_t)M * N >= (1ull << 31))
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: tensor larger than 2 GiB");

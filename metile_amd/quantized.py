@@ -325,9 +325,6 @@ def _swiglu_guards(values, gate_weight, gate_scales, gate_biases, up_weight, up_
             or gate_weight.shape != up_weight.shape or gate_scales.shape != up_scales.shape
             or gate_biases.shape != up_biases.shape):
         raise ValueError("affine SwiGLU requires matching gate/up weights and parameters")
-    if group_size % 64:
-        raise NotImplementedError(
-            "8-bit group-32 affine SwiGLU has no gfx950 kernel yet (groups of 64 and 128 do)")
 
 
 def mlx_affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,

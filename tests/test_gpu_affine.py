@@ -97,6 +97,33 @@ def test_qmv_shapes_and_dtypes(m, k, n, bits, g, dtype):
     _report(f"qmv {dtype} int{bits} g{g} M={m} K={k} N={n}", y, ref, dtype)
 
 
+# Groups of 32: two groups per 64-wide K step (two MFMA chains per step), 16-row chunks, and
+# for long K more K splits (at most 31 steps per split).
+@pytest.mark.parametrize("m,k,n,bits,dtype", [
+    (1, 1024, 160, 4, "bf16"),
+    (5, 1024, 96, 8, "bf16"),
+    (16, 2048, 64, 8, "f16"),
+    (21, 512, 128, 4, "bf16"),    # a 16-row chunk and a 5-row chunk
+    (3, 5120, 256, 8, "bf16"),    # 80 steps -> at least three K splits
+])
+def test_qmv_group32(m, k, n, bits, dtype):
+    y, ref = _qmv_case(m, k, n, bits, 32, dtype=dtype, config_id=m + k + n)
+    _report(f"qmv {dtype} int{bits} g32 M={m} K={k} N={n}", y, ref, dtype)
+
+
+def test_mlp_int8_group32():
+    gate = O.make_affine_weight(384, 256, 8, 32, 6, 10)
+    up = O.make_affine_weight(384, 256, 8, 32, 6, 12)
+    down = O.make_affine_weight(256, 384, 8, 32, 6, 14)
+    x = O.make_activations(4, 256, 6)
+    res = O.make_activations(4, 256, 6, tensor_id=3)
+    ref, _ = O.affine_mlp(x, gate, up, down, 32, 8, residual=res)
+    y = mt.affine_mlp(act_to_torch(x, "bf16"), affine_to_torch(gate, "bf16"),
+                      affine_to_torch(up, "bf16"), affine_to_torch(down, "bf16"),
+                      group_size=32, bits=8, residual=act_to_torch(res, "bf16"))
+    _report("mlp int8 g32 M=4", torch_to_act(y, "bf16"), ref, min_exact=0.85)
+
+
 @pytest.mark.parametrize("m", [1, 5, 32])
 def test_residual_qmv_config1_down(m):
     y, ref = _qmv_case(m, 8960, 1536, 4, 64, config_id=1, residual=True)
@@ -161,7 +188,7 @@ def test_swiglu_config1(m):
     _report(f"swiglu M={m}", torch_to_act(h, "bf16"), ref)
 
 
-@pytest.mark.parametrize("bits,g", [(8, 64), (8, 128)])
+@pytest.mark.parametrize("bits,g", [(8, 64), (8, 128), (8, 32)])
 def test_swiglu_int8(bits, g):
     gate = O.make_affine_weight(512, 1024, bits, g, 4, 10)
     up = O.make_affine_weight(512, 1024, bits, g, 4, 12)
