@@ -1,12 +1,16 @@
 """metile_amd — MI355X (gfx950) kernels for meTile's quantized-projection hot path.
 
 Affine 4/8-bit quantized QMV, fused SwiGLU, the quantized MLP and dense 16-bit small-batch
-projections, written as hand-written HIP kernels behind a C ABI (``include/metile_amd.h``) and exposed here on torch tensors with the
-reference's call surface (``metile/backends/mlx_quantized.py``).
+projections, written as hand-written HIP kernels behind a C ABI (``include/metile_amd.h``) and
+exposed here on torch tensors with the reference's call surface
+(``metile/backends/mlx_quantized.py``), with the reference tuner's fidelity gates and native
+compositions for checking kernels against its semantics.
 """
 
 from ._lib import MetileError, version
 from .dense import DenseWeight, dense_qmv, dense_swiglu, mlx_dense_residual_qmv, mlx_dense_swiglu
+from .fidelity import accuracy_compatible, affine_swiglu_compatible
+from .native import native_affine_matmul, native_affine_residual_qmv, native_affine_swiglu
 from .quantized import (
     AffineWeight,
     affine_dequantize,
@@ -27,6 +31,11 @@ __all__ = [
     "AffineWeight",
     "DenseWeight",
     "MetileError",
+    "accuracy_compatible",
+    "affine_swiglu_compatible",
+    "native_affine_matmul",
+    "native_affine_residual_qmv",
+    "native_affine_swiglu",
     "dense_qmv",
     "dense_swiglu",
     "mlx_dense_residual_qmv",

@@ -348,12 +348,32 @@ def mlx_affine_swiglu_qmv(values, gate_weight, gate_scales, gate_biases, up_weig
                          up_biases, group_size=group_size, bits=bits)
 
 
+def _fidelity_gate(result, reference, what):
+    """Raise unless ``result`` passes the reference tuner's affine fidelity gate against the
+    native composition (``metile/backends/mlx_quantized.py:1256-1272,1297``). The reference
+    falls back to the native path on failure; here a failure is an error."""
+    from .fidelity import affine_swiglu_compatible
+
+    if result.numel() and not affine_swiglu_compatible(result, reference):
+        raise RuntimeError(f"{what}: the gfx950 kernel failed the fidelity gate against the "
+                           "native quantized-matmul composition on the sample input")
+
+
 def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
                                up_scales, up_biases, *, group_size=64, bits=4):
     """Drop-in for ``mlx_affine_swiglu_executor`` (``metile/backends/mlx_quantized.py:1723``):
-    validates once and returns ``execute(values)`` bound to the weights."""
+    validates once, checks the kernel against the native composition on the sample (the
+    reference tuner's fidelity gate) and returns ``execute(values)`` bound to the weights."""
+    from .native import native_affine_swiglu
+
     _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                    up_biases, group_size, bits)
+    _fidelity_gate(
+        affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                      up_biases, group_size=group_size, bits=bits),
+        native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
+                             up_scales, up_biases, group_size=group_size, bits=bits),
+        "affine SwiGLU")
 
     def execute(values):
         return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
@@ -366,14 +386,23 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
                             up_scales, up_biases, down_weight, down_scales, down_biases,
                             sample_residual, *, group_size=64, bits=4):
     """Drop-in for ``mlx_affine_mlp_executor`` (``metile/backends/mlx_quantized.py:1770-1832``):
-    runs the SwiGLU and residual guards on the sample and returns
+    binds the SwiGLU executor (with its fidelity gate), runs the residual guards and the
+    residual stage's fidelity gate on the sample's hidden activation, and returns
     ``execute(values, residual) = down(swiglu(values)) + residual``."""
-    _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
-                   up_biases, group_size, bits)
-    hidden_shape = (*sample_values.shape[:-1], gate_weight.shape[0])
-    probe = torch.empty(hidden_shape, dtype=sample_values.dtype, device="meta")
-    mlx_affine_residual_qmv_guards(probe, down_weight, down_scales, down_biases, sample_residual,
-                                   group_size=group_size, bits=bits)
+    from .native import native_affine_residual_qmv
+
+    swiglu = mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases,
+                                        up_weight, up_scales, up_biases, group_size=group_size,
+                                        bits=bits)
+    hidden = swiglu(sample_values)
+    mlx_affine_residual_qmv_guards(hidden, down_weight, down_scales, down_biases,
+                                   sample_residual, group_size=group_size, bits=bits)
+    _fidelity_gate(
+        affine_qmv(hidden, down_weight, down_scales, down_biases, group_size=group_size,
+                   bits=bits, residual=sample_residual),
+        native_affine_residual_qmv(hidden, down_weight, down_scales, down_biases,
+                                   sample_residual, group_size=group_size, bits=bits),
+        "affine residual QMV")
     gate = (gate_weight, gate_scales, gate_biases)
     up = (up_weight, up_scales, up_biases)
     down = (down_weight, down_scales, down_biases)
