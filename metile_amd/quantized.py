@@ -391,12 +391,18 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
     ``execute(values, residual) = down(swiglu(values)) + residual``."""
     from .native import native_affine_residual_qmv
 
+    # Every argument check first (on a shape-only stand-in for the hidden activation), then
+    # the kernels.
+    _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+                   up_biases, group_size, bits)
+    probe = torch.empty((*sample_values.shape[:-1], gate_weight.shape[0]),
+                        dtype=sample_values.dtype, device="meta")
+    mlx_affine_residual_qmv_guards(probe, down_weight, down_scales, down_biases, sample_residual,
+                                   group_size=group_size, bits=bits)
     swiglu = mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases,
                                         up_weight, up_scales, up_biases, group_size=group_size,
                                         bits=bits)
     hidden = swiglu(sample_values)
-    mlx_affine_residual_qmv_guards(hidden, down_weight, down_scales, down_biases,
-                                   sample_residual, group_size=group_size, bits=bits)
     _fidelity_gate(
         affine_qmv(hidden, down_weight, down_scales, down_biases, group_size=group_size,
                    bits=bits, residual=sample_residual),
