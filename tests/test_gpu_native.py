@@ -60,5 +60,15 @@ def test_executors_gate_their_kernels_on_the_sample():
     r = act_to_torch(O.make_activations(2, 256, 11, tensor_id=3), "bf16")
     ex = mt.mlx_affine_mlp_executor(x, *gate, *up, *down, r)
     y = ex(x, r)
+    # the executor is the two kernels in a row, bit for bit
+    hidden = mt.mlx_affine_swiglu(x, *gate, *up)
+    assert torch.equal(y, mt.mlx_affine_residual_qmv(hidden, *down, r))
+    # the reference gates each stage against its native composition on that stage's input
+    # (metile/backends/mlx_quantized.py:1786-1828): SwiGLU on x, the residual QMV on the
+    # kernel's own hidden activations
+    assert mt.affine_swiglu_compatible(hidden, mt.native_affine_swiglu(x, *gate, *up))
+    assert mt.affine_swiglu_compatible(y, mt.native_affine_residual_qmv(hidden, *down, r))
+    # end to end the two bf16 roundings of the hidden activations compound; the reference
+    # gates no whole-MLP result, so the looser accuracy rule of its dense paths applies here
     want = mt.native_affine_residual_qmv(mt.native_affine_swiglu(x, *gate, *up), *down, r)
-    assert mt.affine_swiglu_compatible(y, want)
+    assert mt.accuracy_compatible(y, want)
