@@ -112,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
       for (int q = 0; q < 4; ++q)
         acc = sum8<DT>(*reinterpret_cast<const u32x4*>(&As[buf][x_row][32 * x_half + 8 * q]), acc);
     }
-    acc += __shfl_xor(acc, 1);
+    acc += dpp_read<kDppXor1>(acc);
     if (x_active && x_half == 0) Xs[buf][x_row] = acc;
   };
 

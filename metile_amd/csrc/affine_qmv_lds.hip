@@ -207,9 +207,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
       const int cc = c - row * cpr;
       // Sum over the chunks of one group: 8 (a whole step) or 4 (a half step).
       float s = sum8<DT>(xv[i], 0.0f);
-      s += __shfl_xor(s, 1);
-      s += __shfl_xor(s, 2);
-      if constexpr (!HALF) s += __shfl_xor(s, 4);
+      s = HALF ? group_sum4(s) : group_sum8(s);
       if (c < nchunks) {
         const u32x4 v = (BITS == 4) ? pair_order(xv[i]) : xv[i];
         *reinterpret_cast<u32x4*>(dyn + lay.x + ((uint32_t)row * xstride + cc * 8) * 2u) = v;

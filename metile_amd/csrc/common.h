@@ -224,6 +224,33 @@ __device__ __forceinline__ float sum8(u32x4 v, float acc) {
   return acc;
 }
 
+// ---- lane exchanges within a row of 16 lanes (DPP: one VALU instruction, no LDS trip) ----
+// kDppXor1 / kDppXor2: lane i reads lane i ^ 1 / i ^ 2 of its quad; kDppHalfMirror: lane i
+// reads lane 7 - i of its group of eight.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_read(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 4 (or 8) lanes; every lane of the group receives it. The
+// additions pair the same operands as xor exchanges over 1, 2 (and 4) would: lanes of a quad
+// hold the same quad sum, so the half mirror's partner quad is the xor-4 one.
+__device__ __forceinline__ float group_sum4(float s) {
+  s += dpp_read<kDppXor1>(s);
+  s += dpp_read<kDppXor2>(s);
+  return s;
+}
+__device__ __forceinline__ float group_sum8(float s) {
+  s = group_sum4(s);
+  s += dpp_read<kDppHalfMirror>(s);
+  return s;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
