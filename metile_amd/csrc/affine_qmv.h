@@ -23,8 +23,10 @@ struct QmvParams {
   int group_shift;           // log2(G / 64)
   int ksplit;
   int steps_per_split;
-  int strips;                // column strips (grid x); the staged kernels take strips of
-                             // N / strips (16..32) columns, the register kernel N / 32
+  int strips;                // column strips; the staged kernels take strips of N / strips
+                             // (16..32) columns, the register kernel N / 32 (grid x = strips)
+  int tiles;                 // staged kernels: strips per workgroup (1 or 2; grid x =
+                             // strips / tiles)
 };
 
 hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,
@@ -34,21 +36,28 @@ hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,
 constexpr int kSbRowWords = kMaxGroupsPerSplit / 2 + 2;
 
 // ---- activation-staged small-row kernels (M <= 16) --------------------------------------
-// Eight waves per workgroup; the workgroup's activation rows for its K range live in LDS.
+// Eight waves per strip ("tile"), one or two tiles per workgroup; the workgroup's activation
+// rows for its K range live in LDS, shared by its tiles.
 constexpr int kQmvLdsWaves = 8;
 constexpr int kQmvLdsMaxRows = 16;
-// Dynamic LDS bound of one workgroup: two workgroups still share a CU's 160 KiB.
-constexpr uint32_t kQmvLdsMaxBytes = 80u * 1024u;
+// Dynamic LDS bound of one workgroup: two one-tile workgroups share a CU's 160 KiB, a two-tile
+// workgroup has the CU to itself (less room for the kernel's static shared variables).
+__host__ __device__ constexpr uint32_t qmv_lds_max_bytes(int tiles) {
+  return tiles == 1 ? 80u * 1024u : 152u * 1024u;
+}
 
-// 16-byte activation chunks each thread stages (M * steps_per_split * 8 chunks in all).
-__host__ __device__ constexpr int qmv_lds_chunk_iters(int mrows) { return mrows <= 8 ? 5 : 8; }
+// 16-byte activation chunks each thread stages (M * steps_per_split * 8 chunks in all, over
+// 512 * tiles threads).
+__host__ __device__ constexpr int qmv_lds_chunk_iters(int mrows, int tiles) {
+  return ((mrows <= 8 ? 5 : 8) + tiles - 1) / tiles;
+}
 
-// Dynamic LDS of one workgroup, byte offsets: scales and biases [2 nproj][32][kSbRowWords]
-// (32-bit words), activation rows [M + 1][steps_per_split * 64 + 8] (16-bit; row M is all
+// Dynamic LDS of one workgroup, byte offsets: scales and biases [tiles][2 nproj][32]
+// [kSbRowWords] (32-bit words), activation rows [M + 1][steps_per_split * 64 + 8] (16-bit; row M is all
 // zeros and stands in for rows M..31 of the MFMA tile), per-step row sums
 // [steps_per_split * halves][mrows] (fp32; halves = 2 for groups of 32, one sum per group).
 // After the K loop the cross-wave reduction buffer
-// [waves][nproj][mrows][33] (fp32) reuses the space from offset 0.
+// [tiles][waves][nproj][mrows][33] (fp32) reuses the space from offset 0.
 struct QmvLdsLayout {
   uint32_t x;
   uint32_t zero;
@@ -57,22 +66,23 @@ struct QmvLdsLayout {
 };
 
 __host__ __device__ inline QmvLdsLayout qmv_lds_layout(int M, int steps_per_split, int mrows,
-                                                       int nproj, int halves) {
+                                                       int nproj, int halves, int tiles) {
   QmvLdsLayout l;
   const uint32_t row = (uint32_t)(steps_per_split * 64 + 8) * 2u;
-  l.x = (uint32_t)(2 * nproj * 32 * kSbRowWords) * 4u;
+  l.x = (uint32_t)(tiles * 2 * nproj * 32 * kSbRowWords) * 4u;
   l.zero = l.x + (uint32_t)M * row;
   l.xsum = l.zero + row;
   const uint32_t staged = l.xsum + (uint32_t)(steps_per_split * halves * mrows) * 4u;
-  const uint32_t red = (uint32_t)(kQmvLdsWaves * nproj * mrows * 33) * 4u;
+  const uint32_t red = (uint32_t)(tiles * kQmvLdsWaves * nproj * mrows * 33) * 4u;
   l.bytes = staged > red ? staged : red;
   return l;
 }
 
 // Whether the activation-staged kernels take M rows split into K ranges of steps_per_split
-// 64-wide steps (the staging must fit the per-thread chunk budget, the scale rows and
-// kQmvLdsMaxBytes). They are the only small-row kernels for groups of 32.
-bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size);
+// 64-wide steps with `tiles` strips per workgroup (the staging must fit the per-thread chunk
+// budget, the scale rows and qmv_lds_max_bytes). They are the only small-row kernels for
+// groups of 32.
+bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size, int tiles);
 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,
                                  hipStream_t stream);

@@ -45,27 +45,36 @@ __device__ __forceinline__ uint16_t quiet_nan() {
   return DT == kBF16 ? (uint16_t)0x7FC0u : (uint16_t)0x7E00u;
 }
 
-// One workgroup's share: output strip `strip` (columns [strip N / strips, (strip + 1) N /
-// strips), at most 32) over K split `split`. Lanes and rows past the strip's width load
-// nothing and store nothing.
+// One workgroup's share: TILES consecutive output strips (strip s = columns [s N / strips,
+// (s + 1) N / strips), at most 32), strips [group TILES, group TILES + TILES), over K split
+// `split`. Each strip is computed by its own eight waves (a tile); the activations of the K
+// split are staged once for all tiles. Lanes and rows past a strip's width load nothing and
+// store nothing.
 // HALF: groups of 32, two per 64-wide K step. Each projection then runs two MFMA chains per
 // step, one per group: lanes of the other K half (h) read the zero row, so each chain sums one
 // group only and gets its own scale, bias and row sum.
-template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE, bool HALF>
-__device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, const int split,
-                                         unsigned char* __restrict__ dyn, int& flag,
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE, bool HALF,
+          int TILES>
+__device__ __forceinline__ void lds_task(const QmvParams& p, const int group, const int split,
+                                         unsigned char* __restrict__ dyn, int* flag,
                                          const MlpLink& link) {
-  constexpr int WAVES = kQmvLdsWaves;
-  constexpr int kThreads = WAVES * 64;
+  static_assert(ROLE == kPlain || TILES == 1, "the one-launch MLP uses one strip per workgroup");
+  constexpr int WAVES = kQmvLdsWaves;  // per tile
+  constexpr int kTileThreads = WAVES * 64;
+  constexpr int kThreads = kTileThreads * TILES;
   constexpr float kOff = CodeOffset<BITS, DT>::value;
   constexpr int kRegs = MROWS / 2;
   constexpr int kArrays = 2 * NPROJ;
-  constexpr int kXIters = qmv_lds_chunk_iters(MROWS);
+  constexpr int kXIters = qmv_lds_chunk_iters(MROWS, TILES);
   constexpr int kHalves = HALF ? 2 : 1;  // row sums (groups) per K step
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave_wg = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = wave_wg / WAVES;
+  const int wave = wave_wg % WAVES;     // within the tile
+  const int ttid = tid % kTileThreads;  // thread within the tile
+  const int strip = group * TILES + tile;
   const int j = lane & 31;
   const int h = lane >> 5;
   const int M = p.M, K = p.K, N = p.N;
@@ -84,9 +93,10 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   const int g_beg = HALF ? 2 * s_beg : s_beg >> gshift;
   const int g_last = HALF ? 2 * s_end - 1 : (s_end - 1) >> gshift;
   const int nwords = (g_last - g_beg + 1) / 2 + 1;
-  const QmvLdsLayout lay = qmv_lds_layout(M, p.steps_per_split, MROWS, NPROJ, kHalves);
+  const QmvLdsLayout lay = qmv_lds_layout(M, p.steps_per_split, MROWS, NPROJ, kHalves, TILES);
   const int xstride = p.steps_per_split * 64 + 8;  // staged row stride, elements
-  uint32_t* sb = reinterpret_cast<uint32_t*>(dyn);  // [kArrays][32][kSbRowWords]
+  // [kArrays][32][kSbRowWords] of this tile
+  uint32_t* sb = reinterpret_cast<uint32_t*>(dyn) + tile * (kArrays * 32 * kSbRowWords);
   float* xsum = reinterpret_cast<float*>(dyn + lay.xsum);  // [steps_per_split * kHalves][MROWS]
 
   const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
@@ -98,9 +108,9 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
 
   // ---- scales and biases: thread t copies 16-byte quads of row t % 32 of every array -----
   constexpr int kQuadsPerRow = (kSbRowWords + 3) / 4;
-  constexpr int kSbIters = (kQuadsPerRow + kThreads / 32 - 1) / (kThreads / 32);
-  const int sb_row = tid & 31;
-  const int sb_q0 = tid >> 5;
+  constexpr int kSbIters = (kQuadsPerRow + kTileThreads / 32 - 1) / (kTileThreads / 32);
+  const int sb_row = ttid & 31;
+  const int sb_q0 = ttid >> 5;
   u32x4 sbv[kArrays][kSbIters];
 #pragma unroll
   for (int a = 0; a < kArrays; ++a) {
@@ -109,18 +119,18 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
     const uint32_t base = (((uint32_t)(col0 + sb_row) * groups_per_row + g_beg) * 2u) & ~3u;
 #pragma unroll
     for (int k = 0; k < kSbIters; ++k) {
-      const int q = sb_q0 + k * (kThreads / 32);
+      const int q = sb_q0 + k * (kTileThreads / 32);
       sbv[a][k] = load16(r, (4 * q < nwords && sb_row < width) ? base + 16u * q : kOOB);
     }
   }
 
   // ---- the residual this thread's output (row tid / 32, column tid % 32) adds, requested now
   // so that the workgroup finishing the strip does not wait for it at the end --------------
-  static_assert(MROWS * 32 <= kThreads, "one output per thread in the epilogue");
+  static_assert(MROWS * 32 <= kTileThreads, "one output per thread in the epilogue");
   uint16_t res_pre = 0;
   if constexpr (NPROJ == 1) {
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.residual, p.residual ? (uint32_t)M * N * 2u : 0u);
-    const int ri = tid >> 5, rc = tid & 31;
+    const int ri = ttid >> 5, rc = ttid & 31;
     res_pre = load2(rr, (ri < M && rc < width) ? ((uint32_t)ri * N + col0 + rc) * 2u : kOOB);
   }
 
@@ -167,10 +177,10 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
         __builtin_amdgcn_s_sleep(2);
         if (++spins == kSpinLimit) break;
       }
-      flag = spins == kSpinLimit;
+      flag[0] = spins == kSpinLimit;
     }
     __syncthreads();
-    return flag != 0;
+    return flag[0] != 0;
   };
   const uint32_t need = (uint32_t)(2 * steps_here);
   if constexpr (ROLE == kDown) {
@@ -192,7 +202,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   for (int a = 0; a < kArrays; ++a)
 #pragma unroll
     for (int k = 0; k < kSbIters; ++k) {
-      const int q = sb_q0 + k * (kThreads / 32);
+      const int q = sb_q0 + k * (kTileThreads / 32);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         if (4 * q + c < kSbRowWords) sb[(a * 32 + sb_row) * kSbRowWords + 4 * q + c] = sbv[a][k][c];
@@ -300,7 +310,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
 
   // ---- cross-wave reduction (fixed order); the buffer reuses the staged data -------------
   __syncthreads();
-  float* red = reinterpret_cast<float*>(dyn);  // [WAVES][NPROJ][MROWS][33]
+  // [WAVES][NPROJ][MROWS][33] of this tile
+  float* red = reinterpret_cast<float*>(dyn) + tile * (WAVES * NPROJ * MROWS * 33);
 #pragma unroll
   for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
@@ -361,7 +372,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
 
   const int outs = M * 32;
   if (p.ksplit == 1) {
-    for (int o = tid; o < outs; o += kThreads) {
+    for (int o = ttid; o < outs; o += kTileThreads) {
       if ((o & 31) >= width) continue;
       float v[NPROJ];
 #pragma unroll
@@ -379,7 +390,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   // or invalidate. Each wave waits for its stores to complete before the barrier, so every
   // partial of this workgroup is visible before the arrival counter moves.
   const size_t plane = (size_t)M * N;
-  for (int o = tid; o < outs; o += kThreads) {
+  for (int o = ttid; o < outs; o += kTileThreads) {
     const int i = o >> 5, c = o & 31;
     if (c >= width) continue;
 #pragma unroll
@@ -390,17 +401,18 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
   }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  if (tid == 0) {
+  if (ttid == 0) {
     const unsigned prev =
         __hip_atomic_fetch_add(&p.counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag = (prev == (unsigned)(p.ksplit - 1));
+    flag[tile] = (prev == (unsigned)(p.ksplit - 1));
   }
   __syncthreads();
-  if (!flag) {
+  // No workgroup barrier follows: one tile may return while the other finishes its strip.
+  if (!flag[tile]) {
     retire();
     return;
   }
-  for (int o = tid; o < outs; o += kThreads) {
+  for (int o = ttid; o < outs; o += kTileThreads) {
     const int i = o >> 5, c = o & 31;
     if (c >= width) continue;
     const size_t oi = (size_t)i * N + col0 + c;
@@ -415,20 +427,21 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int strip, co
     }
     finish(i, c, v);
   }
-  if (tid == 0)
+  if (ttid == 0)
     __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   publish();
   retire();
 }
 
-// At most 128 registers, so that two eight-wave workgroups share a CU.
-template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, bool HALF>
-__global__ __launch_bounds__(kQmvLdsWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
+// At most 128 registers, so that sixteen waves (two one-tile workgroups or one two-tile
+// workgroup) share a CU.
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, bool HALF, int TILES>
+__global__ __launch_bounds__(kQmvLdsWaves * 64 * TILES) __attribute__((amdgpu_waves_per_eu(4)))
 void affine_qmv_lds_kernel(const QmvParams p) {
   extern __shared__ __align__(16) unsigned char dyn_plain[];
-  __shared__ int flag;
+  __shared__ int flag[TILES];
   const MlpLink none{};
-  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain, HALF>(
+  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain, HALF, TILES>(
       p, blockIdx.x, blockIdx.y, dyn_plain, flag, none);
 }
 
@@ -443,36 +456,42 @@ void affine_mlp_kernel(const QmvParams up, const QmvParams down, const MlpLink l
   const int id = blockIdx.x;
   if (id < blocks_up) {
     const int strips = up.strips;
-    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp, false>(up, id % strips,
-                                                                      id / strips, dyn_mlp, flag,
-                                                                      link);
+    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp, false, 1>(
+        up, id % strips, id / strips, dyn_mlp, &flag, link);
   } else {
     const int strips = down.strips;
     const int idd = id - blocks_up;
-    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown, false>(down, idd % strips,
-                                                                  idd / strips, dyn_mlp, flag,
-                                                                  link);
+    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown, false, 1>(
+        down, idd % strips, idd / strips, dyn_mlp, &flag, link);
   }
 }
 
-// Raises a kernel's dynamic LDS limit (64 KiB by default) to kQmvLdsMaxBytes. The launchers
-// call it once per kernel instantiation (a function-local static in each launcher template).
-hipError_t allow_lds(const void* kernel) {
+// Raises a kernel's dynamic LDS limit (64 KiB by default) to what a workgroup of `tiles`
+// strips may use. The launchers call it once per kernel instantiation (a function-local static
+// in each launcher template).
+hipError_t allow_lds(const void* kernel, int tiles) {
   return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)kQmvLdsMaxBytes);
+                             (int)qmv_lds_max_bytes(tiles));
+}
+
+template <int BITS, int DT, int MROWS, int NPROJ, bool HALF, int TILES>
+hipError_t launch_lds_tiles(const QmvParams& p, hipStream_t stream) {
+  // Groups of 32 hold two A operand sets per step, so their ring is shallower.
+  constexpr int kStages = HALF ? (BITS == 4 ? 3 : 2) : (BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4));
+  const QmvLdsLayout lay =
+      qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ, HALF ? 2 : 1, TILES);
+  const dim3 grid(p.strips / TILES, p.ksplit);
+  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages, HALF, TILES>;
+  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel), TILES);
+  if (attr != hipSuccess) return attr;
+  kernel<<<grid, dim3(kQmvLdsWaves * 64 * TILES), lay.bytes, stream>>>(p);
+  return hipGetLastError();
 }
 
 template <int BITS, int DT, int MROWS, int NPROJ, bool HALF>
 hipError_t launch_lds_rows(const QmvParams& p, hipStream_t stream) {
-  // Groups of 32 hold two A operand sets per step, so their ring is shallower.
-  constexpr int kStages = HALF ? (BITS == 4 ? 3 : 2) : (BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4));
-  const QmvLdsLayout lay = qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ, HALF ? 2 : 1);
-  const dim3 grid(p.strips, p.ksplit);
-  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages, HALF>;
-  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
-  if (attr != hipSuccess) return attr;
-  kernel<<<grid, dim3(kQmvLdsWaves * 64), lay.bytes, stream>>>(p);
-  return hipGetLastError();
+  return p.tiles == 2 ? launch_lds_tiles<BITS, DT, MROWS, NPROJ, HALF, 2>(p, stream)
+                      : launch_lds_tiles<BITS, DT, MROWS, NPROJ, HALF, 1>(p, stream);
 }
 
 template <int BITS, int DT, int NPROJ, bool HALF>
@@ -496,12 +515,12 @@ hipError_t launch_lds_bits_dt(const QmvParams& p, int nproj, hipStream_t stream)
 template <int BITS, int DT, int MROWS>
 hipError_t launch_mlp_rows(const QmvParams& up, const QmvParams& down, const MlpLink& link,
                            hipStream_t stream) {
-  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2, 1);
-  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1, 1);
+  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2, 1, 1);
+  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1, 1, 1);
   const int blocks_up = up.strips * up.ksplit;
   const int blocks = blocks_up + link.down_blocks;
   auto kernel = affine_mlp_kernel<BITS, DT, MROWS>;
-  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel));
+  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel), 1);
   if (attr != hipSuccess) return attr;
   kernel<<<dim3(blocks), dim3(kQmvLdsWaves * 64), la.bytes > lb.bytes ? la.bytes : lb.bytes,
            stream>>>(up, down, link, blocks_up);
@@ -517,15 +536,17 @@ hipError_t launch_mlp_bits_dt(const QmvParams& up, const QmvParams& down, const 
 
 }  // namespace
 
-bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size) {
-  if (M < 1 || M > kQmvLdsMaxRows) return false;
+bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size, int tiles) {
+  if (M < 1 || M > kQmvLdsMaxRows || (tiles != 1 && tiles != 2)) return false;
   const int mrows = M <= 8 ? 8 : 16;
-  if (M * steps_per_split * 8 > qmv_lds_chunk_iters(mrows) * kQmvLdsWaves * 64) return false;
+  if (M * steps_per_split * 8 > qmv_lds_chunk_iters(mrows, tiles) * kQmvLdsWaves * 64 * tiles)
+    return false;
   // Groups staged per split (one more may straddle) within the scale rows.
   const int groups = group_size == 32 ? 2 * steps_per_split : steps_per_split;
   if (groups > kMaxGroupsPerSplit - 1) return false;
   const int halves = group_size == 32 ? 2 : 1;
-  return qmv_lds_layout(M, steps_per_split, mrows, nproj, halves).bytes <= kQmvLdsMaxBytes;
+  return qmv_lds_layout(M, steps_per_split, mrows, nproj, halves, tiles).bytes <=
+         qmv_lds_max_bytes(tiles);
 }
 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,

@@ -45,6 +45,7 @@ struct Plan {
   int steps_per_split;
   int strips;
   bool staged;  // activation-staged small-row kernel
+  int tiles;    // staged kernel: strips per workgroup
 };
 
 Plan plan_split(int K, int N) {
@@ -66,6 +67,7 @@ Plan plan_split(int K, int N) {
   p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
   p.strips = strips;
   p.staged = false;
+  p.tiles = 1;
   return p;
 }
 
@@ -75,7 +77,7 @@ Plan plan_split(int K, int N) {
 bool use_lds_path(int rows, int steps_per_split, int nproj, int group_size) {
   const char* env = std::getenv("METILE_AMD_QMV_PATH");
   if (group_size != 32 && env && std::string(env) == "reg") return false;
-  return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size);
+  return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size, 1);
 }
 
 constexpr int kCus = 256;  // compute units of an MI355X
@@ -99,7 +101,7 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
       Plan c = plan;
       c.steps_per_split = (steps + ks - 1) / ks;
       c.ksplit = (steps + c.steps_per_split - 1) / c.steps_per_split;
-      if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size)) {
+      if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size, 1)) {
         plan = c;
         break;
       }
@@ -123,6 +125,18 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
       break;
     }
   }
+  // Two strips per workgroup when the grid is two workgroups per CU: the two strips then share
+  // one staging of the activations (half the activation reads through each CU's memory
+  // pipeline). METILE_AMD_TILES=1 or 2 overrides where the shape allows.
+  const long wgs = (long)plan.strips * plan.ksplit;
+  int tiles = (plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
+  if (const char* t = std::getenv("METILE_AMD_TILES")) {
+    const int forced = std::atoi(t);
+    if (forced == 1 || (forced == 2 && plan.strips % 2 == 0)) tiles = forced;
+  }
+  if (tiles == 2 && !mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 2))
+    tiles = 1;
+  plan.tiles = tiles;
   return plan;
 }
 
@@ -211,6 +225,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
     p.strips = plan.strips;
+    p.tiles = plan.staged ? plan.tiles : 1;
     const hipError_t e = plan.staged ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
                                      : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
     if (e != hipSuccess) return hip_fail(e, op);
@@ -350,10 +365,10 @@ MlpPlan plan_mlp(int M, int H, int I, int group_size) {
   for (; ks <= steps_down; ++ks) {
     down.steps_per_split = (steps_down + ks - 1) / ks;
     down.ksplit = (steps_down + down.steps_per_split - 1) / down.steps_per_split;
-    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1, 64)) break;
+    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1, 64, 1)) break;
   }
   mp.fused = !forced_split && M <= mt::kQmvLdsMaxRows && ks <= steps_down &&
-             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2, 64) && group_size >= 64 &&
+             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2, 64, 1) && group_size >= 64 &&
              strips_up + strips_down + down.ksplit + 1 <= kMaxStrips;
   if (mp.fused) {
     mp.down = down;
