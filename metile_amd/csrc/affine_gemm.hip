@@ -214,10 +214,7 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   for (int o = tid; o < BM * BN; o += 256) {
     const int row = m0 + o / BN, col = n0 + o % BN;
     if (row >= M || col >= N) continue;
-    float v = 0.0f;
-    for (int sp = 0; sp < p.ksplit; ++sp)
-      v += __hip_atomic_load(&p.partial[((size_t)sp * M + row) * N + col], __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    const float v = sum_partials(p.partial + (size_t)row * N + col, (size_t)M * N, p.ksplit);
     p.y[(size_t)row * N + col] = f32_to_act<DT>(v);
   }
   if (tid == 0)

@@ -247,11 +247,7 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
     float v[NPROJ];
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr) {
-      float sacc = 0.0f;
-      for (int sp = 0; sp < p.ksplit; ++sp)
-        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + pr) * plane + oi],
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[pr] = sacc;
+      v[pr] = sum_partials(p.partial + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
     }
     float out;
     if constexpr (NPROJ == 2) {

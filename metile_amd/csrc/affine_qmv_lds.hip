@@ -419,11 +419,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
     float v[NPROJ];
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr) {
-      float sacc = 0.0f;
-      for (int sp = 0; sp < p.ksplit; ++sp)
-        sacc += __hip_atomic_load(&p.partial[(size_t)(sp * NPROJ + pr) * plane + oi],
-                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[pr] = sacc;
+      v[pr] = sum_partials(p.partial + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
     }
     finish(i, c, v);
   }

@@ -251,6 +251,27 @@ __device__ __forceinline__ float group_sum8(float s) {
   return s;
 }
 
+// Sum over sp = 0 .. n - 1 of the device-coherent floats p[sp * stride], added in sp order
+// (split-K partials written by other workgroups). The loads of a batch are issued together, so
+// a batch costs one memory round trip rather than one per term; indices past n re-read the
+// last term and are not added.
+__device__ __forceinline__ float sum_partials(const float* p, size_t stride, int n) {
+  constexpr int kBatch = 8;
+  float acc = 0.0f;
+  for (int b = 0; b < n; b += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int sp = b + u < n ? b + u : n - 1;
+      v[u] = __hip_atomic_load(p + (size_t)sp * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (b + u < n) acc += v[u];
+  }
+  return acc;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
