@@ -470,18 +470,34 @@ hipError_t allow_lds(const void* kernel, int tiles) {
                              (int)qmv_lds_max_bytes(tiles));
 }
 
-template <int BITS, int DT, int MROWS, int NPROJ, bool HALF, int TILES>
-hipError_t launch_lds_tiles(const QmvParams& p, hipStream_t stream) {
-  // Groups of 32 hold two A operand sets per step, so their ring is shallower.
-  constexpr int kStages = HALF ? (BITS == 4 ? 3 : 2) : (BITS == 4 ? 6 : (NPROJ == 2 ? 3 : 4));
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, bool HALF, int TILES>
+hipError_t launch_lds_stages(const QmvParams& p, hipStream_t stream) {
   const QmvLdsLayout lay =
       qmv_lds_layout(p.M, p.steps_per_split, MROWS, NPROJ, HALF ? 2 : 1, TILES);
   const dim3 grid(p.strips / TILES, p.ksplit);
-  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, kStages, HALF, TILES>;
+  auto kernel = affine_qmv_lds_kernel<BITS, DT, MROWS, NPROJ, STAGES, HALF, TILES>;
   static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel), TILES);
   if (attr != hipSuccess) return attr;
   kernel<<<grid, dim3(kQmvLdsWaves * 64 * TILES), lay.bytes, stream>>>(p);
   return hipGetLastError();
+}
+
+// Code ring depth: for 4-bit codes six stages, or three when no wave has more than three K
+// steps (the common one-split K = 1536): every stage past a wave's last step is still issued
+// as an out-of-range load, and those measured about 0.9 us per launch at that shape. Groups
+// of 32 hold two A operand sets per step, so their ring is shallower.
+template <int BITS, int DT, int MROWS, int NPROJ, bool HALF, int TILES>
+hipError_t launch_lds_tiles(const QmvParams& p, hipStream_t stream) {
+  if constexpr (HALF) {
+    return launch_lds_stages<BITS, DT, MROWS, NPROJ, BITS == 4 ? 3 : 2, HALF, TILES>(p, stream);
+  } else if constexpr (BITS == 8) {
+    return launch_lds_stages<BITS, DT, MROWS, NPROJ, NPROJ == 2 ? 3 : 4, HALF, TILES>(p, stream);
+  } else {
+    const int steps = min(p.steps_per_split, p.K / 64);
+    const int per_wave = (steps + kQmvLdsWaves - 1) / kQmvLdsWaves;
+    return per_wave <= 3 ? launch_lds_stages<BITS, DT, MROWS, NPROJ, 3, HALF, TILES>(p, stream)
+                         : launch_lds_stages<BITS, DT, MROWS, NPROJ, 6, HALF, TILES>(p, stream);
+  }
 }
 
 template <int BITS, int DT, int MROWS, int NPROJ, bool HALF>
