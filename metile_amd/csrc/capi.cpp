@@ -82,6 +82,14 @@ bool use_lds_path(int rows, int steps_per_split, int nproj, int group_size) {
 
 constexpr int kCus = 256;  // compute units of an MI355X
 
+// Code ring depth of the staged kernel for a shape (the stage counts its launcher picks; the
+// 4-bit ring is six stages deep, or three when every wave has at most three K steps).
+int staged_ring(int bits, int nproj, int group_size) {
+  if (group_size == 32) return bits == 4 ? 3 : 2;
+  if (bits == 8) return nproj == 2 ? 3 : 4;
+  return 6;
+}
+
 // Plan of one small-row call chunk of `rows` rows: the split plan, and for the staged kernel
 // a strip count that evens out the CUs. Its column strips need not be 32 wide: a workgroup
 // takes columns [s N / strips, (s + 1) N / strips) (16 to 32 of them; the MFMA tile masks
@@ -92,7 +100,7 @@ constexpr int kCus = 256;  // compute units of an MI355X
 // are rebalanced: a grid of several rounds evens out as workgroups retire, and its narrower
 // strips measured slower. (Changing the K split instead also measured slower: every split
 // adds a partial-sum hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
-Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
+Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   Plan plan = plan_split(K, N);
   if (group_size == 32) {
     // Two groups per K step: split K until the staged kernel's scale rows and LDS take it.
@@ -105,6 +113,37 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
         plan = c;
         break;
       }
+    }
+  }
+  // Split K further where that puts the rows on the staged kernel (its activation staging
+  // holds M * steps_per_split * 8 chunks), at most to twice the planned split; and in grids of
+  // several rounds of workgroups anyway, until every wave's K steps fit its code ring (a ring
+  // that refills costs more than the extra split: K = 5120, N = 17408 at 8 bits measured
+  // 30.3 us with 3 splits against 32.7 us with 2). A forced METILE_AMD_KSPLIT is kept.
+  if (!std::getenv("METILE_AMD_KSPLIT") && group_size != 32) {
+    const int steps = K / 64;
+    auto split_into = [&](int ks) {
+      Plan c = plan;
+      c.steps_per_split = (steps + ks - 1) / ks;
+      c.ksplit = (steps + c.steps_per_split - 1) / c.steps_per_split;
+      return c;
+    };
+    if (!mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 1)) {
+      for (int ks = plan.ksplit + 1; ks <= 2 * plan.ksplit && ks <= steps; ++ks) {
+        const Plan c = split_into(ks);
+        if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size, 1)) {
+          plan = c;
+          break;
+        }
+      }
+    }
+    const int ring = staged_ring(bits, nproj, group_size);
+    for (int ks = plan.ksplit; (long)(N / 32) * ks > 2L * kCus && ks < steps; ++ks) {
+      const Plan c = split_into(ks);
+      if (c.ksplit < plan.ksplit) continue;
+      if (!mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size, 1)) break;
+      plan = c;
+      if ((c.steps_per_split + mt::kQmvLdsWaves - 1) / mt::kQmvLdsWaves <= ring) break;
     }
   }
   if (!use_lds_path(rows, plan.steps_per_split, nproj, group_size)) return plan;
@@ -144,13 +183,13 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size) {
 // staged kernel's largest row bucket).
 int row_chunk(int group_size) { return group_size == 32 ? mt::kQmvLdsMaxRows : kRowChunk; }
 
-size_t qmv_workspace(int M, int K, int N, int nproj, int group_size) {
+size_t qmv_workspace(int M, int K, int N, int nproj, int group_size, int bits) {
   // Row chunks and one remainder chunk may plan differently.
   const int chunk = row_chunk(group_size);
   size_t need = 0;
   for (int rows : {M < chunk ? M : chunk, M % chunk}) {
     if (rows < 1) continue;
-    const Plan plan = plan_qmv(rows, K, N, nproj, group_size);
+    const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits);
     if (plan.ksplit <= 1) continue;
     const size_t b = kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
     if (b > need) need = b;
@@ -192,7 +231,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     if (!w[q] || !s[q] || !b[q])
       return fail(MT_ERR_INVALID_ARGUMENT,
                   std::string(op) + ": null packed weight, scales or biases");
-  const size_t need = qmv_workspace(M, K, N, nproj, group_size);
+  const size_t need = qmv_workspace(M, K, N, nproj, group_size, bits);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
@@ -200,7 +239,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
   const int chunk = row_chunk(group_size);
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int rows = (M - r0) < chunk ? (M - r0) : chunk;
-    const Plan plan = plan_qmv(rows, K, N, nproj, group_size);
+    const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits);
     if (group_size == 32 && !plan.staged)
       return fail(MT_ERR_INVALID_ARGUMENT,
                   std::string(op) + ": no staged plan fits groups of 32 at this shape");
@@ -345,7 +384,7 @@ struct MlpPlan {
   size_t up_partial, down_partial, hidden, bytes;  // workspace offsets (bytes) and total
 };
 
-MlpPlan plan_mlp(int M, int H, int I, int group_size) {
+MlpPlan plan_mlp(int M, int H, int I, int group_size, int bits) {
   MlpPlan mp{};
   mp.up = plan_split(H, I);
   mp.down = plan_split(I, H);
@@ -380,8 +419,8 @@ MlpPlan plan_mlp(int M, int H, int I, int group_size) {
         mp.down.ksplit > 1 ? align_up((size_t)mp.down.ksplit * M * H * 4) : 0;
     mp.hidden = mp.down_partial + down_bytes;
   } else {
-    const size_t a = qmv_workspace(M, H, I, 2, group_size);
-    const size_t b = qmv_workspace(M, I, H, 1, group_size);
+    const size_t a = qmv_workspace(M, H, I, 2, group_size, bits);
+    const size_t b = qmv_workspace(M, I, H, 1, group_size, bits);
     const size_t split = align_up(a > b ? a : b);
     mp.hidden = split > kCounterBytes ? split : kCounterBytes;
   }
@@ -400,7 +439,7 @@ const char* mt_last_error(void) { return g_last_error.c_str(); }
 size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj) {
   if (check_affine("mt_affine_qmv_workspace_bytes", M, K, N, group_size, bits, MT_BF16))
     return 0;
-  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1, group_size);
+  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1, group_size, bits);
 }
 
 int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
@@ -428,7 +467,7 @@ size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bi
   if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
       check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
     return 0;
-  return plan_mlp(M, H, I, group_size).bytes;
+  return plan_mlp(M, H, I, group_size, bits).bytes;
 }
 
 int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
@@ -448,7 +487,7 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   if (!x || !y || !gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases ||
       !down_w || !down_scales || !down_biases)
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_mlp: null pointer");
-  const MlpPlan mp = plan_mlp(M, H, I, group_size);
+  const MlpPlan mp = plan_mlp(M, H, I, group_size, bits);
   char* ws = static_cast<char*>(workspace);
   void* h = ws + mp.hidden;
   if (!mp.fused) {
