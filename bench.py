@@ -407,7 +407,7 @@ def main():
         "rows": rows_out,
         "roofline": {
             "bound": "hbm",
-            "kernel": "affine_qmv_lds_kernel<4,bf16,8,2> (fused gate/up SwiGLU), M=1",
+            "kernel": "affine_qmv_lds_kernel<4, 0, 8, 2, 3, false, 2> (fused gate/up SwiGLU), M=1",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
