@@ -87,6 +87,38 @@ int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* bi
                          float* out, int N, int K, int group_size, int bits, int dtype,
                          void* stream);
 
+/* ---- ahead-of-time repack for the small-row kernels --------------------------------------- */
+
+/* Step-major repack of MLX affine codes: the 8*bits bytes holding codes [64t, 64t + 64) of row
+ * n move to byte (t*N + n)*8*bits of `out` (same size as w_q, 16-byte aligned buffers), so the
+ * codes all columns of a strip need for one K step are contiguous. Scales and biases keep their
+ * [N, K/group_size] layout. Replaces repack_mlx_affine_weight
+ * (metile/backends/mlx_quantized.py:754-774), whose K-major nibble layout feeds the reference's
+ * NAX kernels; this one is laid out for these kernels' loads. bits in {4, 8}; K % 64 == 0. */
+int mt_affine_repack(const uint32_t* w_q, uint32_t* out, int N, int K, int bits, void* stream);
+
+/* mt_affine_qmv, mt_affine_swiglu and mt_affine_mlp over repacked codes (mt_affine_repack);
+ * same arguments, shape rules, workspace sizes and results, bit for bit. Replace the
+ * reference's entries over pre-repacked weights, mlx_affine_qmv_nax and
+ * mlx_affine_swiglu_qmv_nax (metile/backends/mlx_quantized.py:777-831), and the repacked
+ * path its executors take (metile/backends/mlx_quantized.py:949-967,1082-1100). */
+int mt_affine_qmv_repacked(const void* x, const uint32_t* w_packed, const void* scales,
+                           const void* biases, const void* residual, void* y, int M, int K, int N,
+                           int group_size, int bits, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int mt_affine_swiglu_repacked(const void* x, const uint32_t* gate_packed, const void* gate_scales,
+                              const void* gate_biases, const uint32_t* up_packed,
+                              const void* up_scales, const void* up_biases, void* h, int M, int K,
+                              int N, int group_size, int bits, int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+int mt_affine_mlp_repacked(const void* x, const uint32_t* gate_packed, const void* gate_scales,
+                           const void* gate_biases, const uint32_t* up_packed,
+                           const void* up_scales, const void* up_biases,
+                           const uint32_t* down_packed, const void* down_scales,
+                           const void* down_biases, const void* residual, void* y, int M, int H,
+                           int I, int group_size, int bits, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ---- prefill (many rows) ---------------------------------------------------------------- */
 
 /* Workspace bytes mt_affine_gemm needs (0 when K is not split). */

@@ -17,14 +17,18 @@ from .quantized import (
     affine_matmul,
     affine_mlp,
     affine_qmv,
+    affine_repack,
     affine_swiglu,
     mlx_affine_matmul,
     mlx_affine_mlp_executor,
     mlx_affine_qmv,
+    mlx_affine_qmv_nax,
     mlx_affine_residual_qmv,
     mlx_affine_swiglu,
     mlx_affine_swiglu_executor,
     mlx_affine_swiglu_qmv,
+    mlx_affine_swiglu_qmv_nax,
+    repack_mlx_affine_weight,
 )
 
 __all__ = [
@@ -44,13 +48,17 @@ __all__ = [
     "affine_matmul",
     "affine_mlp",
     "affine_qmv",
+    "affine_repack",
     "affine_swiglu",
     "mlx_affine_matmul",
     "mlx_affine_mlp_executor",
     "mlx_affine_qmv",
+    "mlx_affine_qmv_nax",
     "mlx_affine_residual_qmv",
     "mlx_affine_swiglu",
     "mlx_affine_swiglu_executor",
     "mlx_affine_swiglu_qmv",
+    "mlx_affine_swiglu_qmv_nax",
+    "repack_mlx_affine_weight",
     "version",
 ]

@@ -36,6 +36,12 @@ SIGNATURES = {
     "mt_affine_mlp": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                            _I, _P, _Z, _P]),
     "mt_affine_dequantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "mt_affine_repack": (_I, [_P, _P, _I, _I, _I, _P]),
+    "mt_affine_qmv_repacked": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
+    "mt_affine_swiglu_repacked": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                       _P, _Z, _P]),
+    "mt_affine_mlp_repacked": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                    _I, _I, _I, _P, _Z, _P]),
     "mt_affine_gemm_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "mt_affine_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_stream_read": (_I, [_P, _Z, _P, _I, _P]),

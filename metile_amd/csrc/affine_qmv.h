@@ -27,7 +27,18 @@ struct QmvParams {
                              // (16..32) columns, the register kernel N / 32 (grid x = strips)
   int tiles;                 // staged kernels: strips per workgroup (1 or 2; grid x =
                              // strips / tiles)
+  // Code layout, as byte strides of a column's codes and of one 64-wide K step: MLX rows
+  // (column stride K * bits / 8, step stride 8 * bits) or the step-major repack (column stride
+  // 8 * bits, step stride N * 8 * bits; see launch_affine_repack).
+  uint32_t col_stride;
+  uint32_t step_stride;
 };
+
+// Step-major repack of MLX affine codes: the 8 * bits bytes of column n and K step t (codes
+// [64 t, 64 t + 64) of row n) move to byte (t * N + n) * 8 * bits, so the codes every column of
+// a strip needs for one K step are contiguous.
+hipError_t launch_affine_repack(const uint32_t* w, uint32_t* out, int N, int K, int bits,
+                                hipStream_t stream);
 
 hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,
                              hipStream_t stream);

@@ -110,7 +110,7 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
   }
 
   // ---- weight and activation pipeline ----------------------------------------------------
-  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + (uint32_t)h * 4u * BITS;
+  const uint32_t w_row = (uint32_t)(strip * 32 + j) * p.col_stride + (uint32_t)h * 4u * BITS;
   const uint32_t x_row = j < M ? ((uint32_t)j * K + 32u * h) * 2u : kOOB;
 
   Stage<BITS, NPROJ> ring[STAGES];
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
   // need no branch and every wait stays exact.
   auto load_stage = [&](Stage<BITS, NPROJ>& S, int st) {
     const bool ok = st < w_end;
-    const uint32_t woff = ok ? w_row + (uint32_t)st * 8u * BITS : kOOB;
+    const uint32_t woff = ok ? w_row + (uint32_t)st * p.step_stride : kOOB;
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
@@ -357,6 +357,42 @@ hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* s, const 
     else
       affine_dequantize_kernel<8, kF16><<<blocks, 256, 0, stream>>>(w, s, b, out, N, K, G);
   }
+  return hipGetLastError();
+}
+
+// ---- step-major repack ---------------------------------------------------------------------
+
+namespace {
+
+// Thread i writes 16-byte piece i of the repacked buffer: piece q of the chunk of column n and
+// K step t, where chunk c = t * N + n holds `pieces` pieces.
+__global__ __launch_bounds__(256) void affine_repack_kernel(const u32x4* __restrict__ w,
+                                                            u32x4* __restrict__ out, int N,
+                                                            int steps, int pieces) {
+  const size_t total = (size_t)N * steps * pieces;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * blockDim.x) {
+    const size_t c = i / pieces;
+    const int q = (int)(i - c * pieces);
+    const int t = (int)(c / N);
+    const int n = (int)(c - (size_t)t * N);
+    out[i] = w[((size_t)n * steps + t) * pieces + q];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_affine_repack(const uint32_t* w, uint32_t* out, int N, int K, int bits,
+                                hipStream_t stream) {
+  const int steps = K / 64;
+  const int pieces = bits / 2;  // a chunk is 8 * bits bytes
+  const size_t total = (size_t)N * steps * pieces;
+  const size_t want = (total + 255) / 256;
+  const int blocks = (int)(want < 8192 ? want : 8192);
+  if (blocks == 0) return hipSuccess;
+  affine_repack_kernel<<<blocks, 256, 0, stream>>>(reinterpret_cast<const u32x4*>(w),
+                                                   reinterpret_cast<u32x4*>(out), N, steps,
+                                                   pieces);
   return hipGetLastError();
 }
 

@@ -154,12 +154,12 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
 
   // ---- code ring ---------------------------------------------------------------------------
   const uint32_t w_row =
-      j < width ? (uint32_t)(col0 + j) * row_bytes + (uint32_t)h * 4u * BITS : kOOB;
+      j < width ? (uint32_t)(col0 + j) * p.col_stride + (uint32_t)h * 4u * BITS : kOOB;
   typedef u32x4 StageW[NPROJ][BITS / 4];
   StageW ring[STAGES];
   auto load_stage = [&](StageW& S, int st) {
     const bool ok = st < w_end;
-    const uint32_t woff = (ok && w_row != kOOB) ? w_row + (uint32_t)st * 8u * BITS : kOOB;
+    const uint32_t woff = (ok && w_row != kOOB) ? w_row + (uint32_t)st * p.step_stride : kOOB;
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll

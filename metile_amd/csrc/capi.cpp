@@ -164,11 +164,13 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
       break;
     }
   }
-  // Two strips per workgroup when the grid is two workgroups per CU: the two strips then share
-  // one staging of the activations (half the activation reads through each CU's memory
-  // pipeline). METILE_AMD_TILES=1 or 2 overrides where the shape allows.
+  // Two strips per workgroup when the grid is two workgroups per CU and there are more than 8
+  // rows: the two strips then share one staging of the activations (half the activation
+  // reads through each CU's memory pipeline). At 8 rows or fewer that staging is small and
+  // the 16-wave workgroup measured slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us).
+  // METILE_AMD_TILES=1 or 2 overrides where the shape allows.
   const long wgs = (long)plan.strips * plan.ksplit;
-  int tiles = (plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
+  int tiles = (rows > 8 && plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
   if (const char* t = std::getenv("METILE_AMD_TILES")) {
     const int forced = std::atoi(t);
     if (forced == 1 || (forced == 2 && plan.strips % 2 == 0)) tiles = forced;
@@ -220,10 +222,24 @@ int check_affine(const char* op, int M, int K, int N, int group_size, int bits, 
   return MT_OK;
 }
 
+// Code layouts the small-row kernels read: MLX's output-major words, or the step-major repack
+// of mt_affine_repack.
+enum CodeLayout : int { kLayoutMlx = 0, kLayoutStepMajor = 1 };
+
+void set_layout(mt::QmvParams& p, int layout, int bits) {
+  if (layout == kLayoutStepMajor) {
+    p.col_stride = 8u * (uint32_t)bits;
+    p.step_stride = (uint32_t)p.N * 8u * (uint32_t)bits;
+  } else {
+    p.col_stride = (uint32_t)p.K * (uint32_t)bits / 8u;
+    p.step_stride = 8u * (uint32_t)bits;
+  }
+}
+
 int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2],
             const void* const s[2], const void* const b[2], const void* residual, void* y,
             int M, int K, int N, int group_size, int bits, int dtype, void* workspace,
-            size_t workspace_bytes, void* stream) {
+            size_t workspace_bytes, void* stream, int layout) {
   int st = check_affine(op, M, K, N, group_size, bits, dtype);
   if (st) return st;
   if (!x || !y) return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null x or output");
@@ -265,6 +281,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.steps_per_split = plan.steps_per_split;
     p.strips = plan.strips;
     p.tiles = plan.staged ? plan.tiles : 1;
+    set_layout(p, layout, bits);
     const hipError_t e = plan.staged ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
                                      : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
     if (e != hipSuccess) return hip_fail(e, op);
@@ -430,73 +447,59 @@ MlpPlan plan_mlp(int M, int H, int I, int group_size, int bits) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-const char* mt_version(void) { return "metile_amd 0.1.0 (gfx950)"; }
-
-const char* mt_last_error(void) { return g_last_error.c_str(); }
-
-size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj) {
-  if (check_affine("mt_affine_qmv_workspace_bytes", M, K, N, group_size, bits, MT_BF16))
-    return 0;
-  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1, group_size, bits);
-}
-
-int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
-                  const void* residual, void* y, int M, int K, int N, int group_size, int bits,
-                  int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+int affine_qmv_impl(const char* op, const void* x, const uint32_t* w_q, const void* scales,
+                    const void* biases, const void* residual, void* y, int M, int K, int N,
+                    int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
+                    void* stream, int layout) {
   const uint32_t* w[2] = {w_q, nullptr};
   const void* s[2] = {scales, nullptr};
   const void* b[2] = {biases, nullptr};
-  return run_qmv("mt_affine_qmv", 1, x, w, s, b, residual, y, M, K, N, group_size, bits, dtype,
-                 workspace, workspace_bytes, stream);
+  return run_qmv(op, 1, x, w, s, b, residual, y, M, K, N, group_size, bits, dtype, workspace,
+                 workspace_bytes, stream, layout);
 }
 
-int mt_affine_swiglu(const void* x, const uint32_t* gate_w, const void* gate_scales,
-                     const void* gate_biases, const uint32_t* up_w, const void* up_scales,
-                     const void* up_biases, void* h, int M, int K, int N, int group_size,
-                     int bits, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+int affine_swiglu_impl(const char* op, const void* x, const uint32_t* gate_w,
+                       const void* gate_scales, const void* gate_biases, const uint32_t* up_w,
+                       const void* up_scales, const void* up_biases, void* h, int M, int K, int N,
+                       int group_size, int bits, int dtype, void* workspace,
+                       size_t workspace_bytes, void* stream, int layout) {
   const uint32_t* w[2] = {gate_w, up_w};
   const void* s[2] = {gate_scales, up_scales};
   const void* b[2] = {gate_biases, up_biases};
-  return run_qmv("mt_affine_swiglu", 2, x, w, s, b, nullptr, h, M, K, N, group_size, bits,
-                 dtype, workspace, workspace_bytes, stream);
+  return run_qmv(op, 2, x, w, s, b, nullptr, h, M, K, N, group_size, bits, dtype, workspace,
+                 workspace_bytes, stream, layout);
 }
 
-size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bits) {
-  if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
-      check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
-    return 0;
-  return plan_mlp(M, H, I, group_size, bits).bytes;
-}
-
-int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
-                  const void* gate_biases, const uint32_t* up_w, const void* up_scales,
-                  const void* up_biases, const uint32_t* down_w, const void* down_scales,
-                  const void* down_biases, const void* residual, void* y, int M, int H, int I,
-                  int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
-                  void* stream) {
-  int st = check_affine("mt_affine_mlp", M, H, I, group_size, bits, dtype);
+int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
+                    const void* gate_scales, const void* gate_biases, const uint32_t* up_w,
+                    const void* up_scales, const void* up_biases, const uint32_t* down_w,
+                    const void* down_scales, const void* down_biases, const void* residual,
+                    void* y, int M, int H, int I, int group_size, int bits, int dtype,
+                    void* workspace, size_t workspace_bytes, void* stream, int layout) {
+  int st = check_affine(op, M, H, I, group_size, bits, dtype);
   if (st) return st;
-  st = check_affine("mt_affine_mlp", M, I, H, group_size, bits, dtype);
+  st = check_affine(op, M, I, H, group_size, bits, dtype);
   if (st) return st;
-  const size_t need = mt_affine_mlp_workspace_bytes(M, H, I, group_size, bits);
+  const size_t need = plan_mlp(M, H, I, group_size, bits).bytes;
   if (!workspace || workspace_bytes < need)
-    return fail(MT_ERR_WORKSPACE, "mt_affine_mlp: workspace of " + std::to_string(need) +
+    return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
   if (!x || !y || !gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases ||
       !down_w || !down_scales || !down_biases)
-    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_mlp: null pointer");
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null pointer");
   const MlpPlan mp = plan_mlp(M, H, I, group_size, bits);
   char* ws = static_cast<char*>(workspace);
   void* h = ws + mp.hidden;
   if (!mp.fused) {
     // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
-    st = mt_affine_swiglu(x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h, M,
-                          H, I, group_size, bits, dtype, workspace, mp.hidden, stream);
+    st = affine_swiglu_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
+                            h, M, H, I, group_size, bits, dtype, workspace, mp.hidden, stream,
+                            layout);
     if (st) return st;
-    return mt_affine_qmv(h, down_w, down_scales, down_biases, residual, y, M, I, H, group_size,
-                         bits, dtype, workspace, mp.hidden, stream);
+    return affine_qmv_impl(op, h, down_w, down_scales, down_biases, residual, y, M, I, H,
+                           group_size, bits, dtype, workspace, mp.hidden, stream, layout);
   }
   // [counters: gate/up strips | down strips | ready[] | done][gate/up partials]
   // [down partials][hidden activation]
@@ -535,6 +538,8 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   down.strips = strips_down;
   up.G = down.G = group_size;
   up.group_shift = down.group_shift = __builtin_ctz((unsigned)(group_size / 64));
+  set_layout(up, layout, bits);
+  set_layout(down, layout, bits);
   mt::MlpLink link{};
   link.ready = counters + strips_up + strips_down;
   link.done = link.ready + mp.down.ksplit;
@@ -544,8 +549,107 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   if (const char* env = std::getenv("METILE_AMD_MLP_PREFETCH_AT")) link.prefetch_at = std::atoi(env);
   const hipError_t e = mt::launch_affine_mlp_fused(up, down, link, bits, dtype,
                                                    static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, "mt_affine_mlp");
+  if (e != hipSuccess) return hip_fail(e, op);
   return MT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mt_version(void) { return "metile_amd 0.1.0 (gfx950)"; }
+
+const char* mt_last_error(void) { return g_last_error.c_str(); }
+
+size_t mt_affine_qmv_workspace_bytes(int M, int K, int N, int group_size, int bits, int nproj) {
+  if (check_affine("mt_affine_qmv_workspace_bytes", M, K, N, group_size, bits, MT_BF16))
+    return 0;
+  return qmv_workspace(M, K, N, nproj == 2 ? 2 : 1, group_size, bits);
+}
+
+int mt_affine_qmv(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
+                  const void* residual, void* y, int M, int K, int N, int group_size, int bits,
+                  int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return affine_qmv_impl("mt_affine_qmv", x, w_q, scales, biases, residual, y, M, K, N,
+                         group_size, bits, dtype, workspace, workspace_bytes, stream, kLayoutMlx);
+}
+
+int mt_affine_swiglu(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                     const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                     const void* up_biases, void* h, int M, int K, int N, int group_size,
+                     int bits, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return affine_swiglu_impl("mt_affine_swiglu", x, gate_w, gate_scales, gate_biases, up_w,
+                            up_scales, up_biases, h, M, K, N, group_size, bits, dtype, workspace,
+                            workspace_bytes, stream, kLayoutMlx);
+}
+
+size_t mt_affine_mlp_workspace_bytes(int M, int H, int I, int group_size, int bits) {
+  if (check_affine("mt_affine_mlp_workspace_bytes", M, H, I, group_size, bits, MT_BF16) ||
+      check_affine("mt_affine_mlp_workspace_bytes", M, I, H, group_size, bits, MT_BF16))
+    return 0;
+  return plan_mlp(M, H, I, group_size, bits).bytes;
+}
+
+int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                  const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                  const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                  const void* down_biases, const void* residual, void* y, int M, int H, int I,
+                  int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  return affine_mlp_impl("mt_affine_mlp", x, gate_w, gate_scales, gate_biases, up_w, up_scales,
+                         up_biases, down_w, down_scales, down_biases, residual, y, M, H, I,
+                         group_size, bits, dtype, workspace, workspace_bytes, stream,
+                         kLayoutMlx);
+}
+
+int mt_affine_repack(const uint32_t* w_q, uint32_t* out, int N, int K, int bits, void* stream) {
+  if (bits != 4 && bits != 8)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_repack: bits must be 4 or 8");
+  if (N < 1 || K < 64 || K % 64)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "mt_affine_repack: N must be positive and K a positive multiple of 64");
+  if (!w_q || !out)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_repack: null pointer");
+  if ((reinterpret_cast<uintptr_t>(w_q) | reinterpret_cast<uintptr_t>(out)) & 15u)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_repack: buffers must be 16-byte aligned");
+  if ((size_t)N * K * bits / 8 >= (1ull << 31))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_repack: tensor larger than 2 GiB");
+  const hipError_t e =
+      mt::launch_affine_repack(w_q, out, N, K, bits, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_affine_repack");
+  return MT_OK;
+}
+
+int mt_affine_qmv_repacked(const void* x, const uint32_t* w_packed, const void* scales,
+                           const void* biases, const void* residual, void* y, int M, int K, int N,
+                           int group_size, int bits, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return affine_qmv_impl("mt_affine_qmv_repacked", x, w_packed, scales, biases, residual, y, M, K,
+                         N, group_size, bits, dtype, workspace, workspace_bytes, stream,
+                         kLayoutStepMajor);
+}
+
+int mt_affine_swiglu_repacked(const void* x, const uint32_t* gate_packed, const void* gate_scales,
+                              const void* gate_biases, const uint32_t* up_packed,
+                              const void* up_scales, const void* up_biases, void* h, int M, int K,
+                              int N, int group_size, int bits, int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  return affine_swiglu_impl("mt_affine_swiglu_repacked", x, gate_packed, gate_scales, gate_biases,
+                            up_packed, up_scales, up_biases, h, M, K, N, group_size, bits, dtype,
+                            workspace, workspace_bytes, stream, kLayoutStepMajor);
+}
+
+int mt_affine_mlp_repacked(const void* x, const uint32_t* gate_packed, const void* gate_scales,
+                           const void* gate_biases, const uint32_t* up_packed,
+                           const void* up_scales, const void* up_biases,
+                           const uint32_t* down_packed, const void* down_scales,
+                           const void* down_biases, const void* residual, void* y, int M, int H,
+                           int I, int group_size, int bits, int dtype, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return affine_mlp_impl("mt_affine_mlp_repacked", x, gate_packed, gate_scales, gate_biases,
+                         up_packed, up_scales, up_biases, down_packed, down_scales, down_biases,
+                         residual, y, M, H, I, group_size, bits, dtype, workspace,
+                         workspace_bytes, stream, kLayoutStepMajor);
 }
 
 int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,

@@ -9,7 +9,10 @@ effect on the result).
 
 Tensor formats (MLX affine): ``weight`` uint32 (or int32 holding the same bits)
 ``[N, K*bits/32]``; ``scales``/``biases`` ``[N, K/group_size]`` in the activation dtype
-(bfloat16 or float16); activations ``[..., K]``.
+(bfloat16 or float16); activations ``[..., K]``. ``affine_qmv``, ``affine_swiglu`` and
+``affine_mlp`` also take codes repacked ahead of time by ``affine_repack`` (step-major
+``[K/64, N, 2*bits]``; the layout is told apart by the number of dimensions) and then give the
+same results bit for bit.
 """
 
 from __future__ import annotations
@@ -74,12 +77,26 @@ def _dtype_code(dtype: torch.dtype) -> int:
         raise ValueError("activations must be bfloat16 or float16") from None
 
 
+def _repacked(weight) -> bool:
+    """Codes in the step-major repack of ``affine_repack`` rather than MLX's rows."""
+    return weight.ndim == 3
+
+
+def _code_shape(weight, bits):
+    """``(N, K)`` of packed codes in either layout, or ``None`` if the shape is neither."""
+    if weight.ndim == 2:
+        return weight.shape[0], weight.shape[1] * 32 // bits
+    if weight.ndim == 3 and weight.shape[2] == 2 * bits:
+        return weight.shape[1], weight.shape[0] * 64
+    return None
+
+
 def _check_params(values, weight, scales, biases, group_size, bits, what):
     k = values.shape[-1]
-    n = weight.shape[0]
-    if (weight.ndim != 2 or weight.shape[1] * 32 // bits != k
-            or tuple(scales.shape) != (n, k // group_size)
-            or tuple(biases.shape) != (n, k // group_size)):
+    shape = _code_shape(weight, bits)
+    if (shape is None or shape[1] != k
+            or tuple(scales.shape) != (shape[0], k // group_size)
+            or tuple(biases.shape) != (shape[0], k // group_size)):
         raise ValueError(f"{what} received incompatible quantization parameters")
     if scales.dtype != values.dtype or biases.dtype != values.dtype:
         raise ValueError(f"{what} parameters must match the input dtype")
@@ -103,7 +120,7 @@ def affine_qmv(values, weight, scales, biases, *, group_size=64, bits=4, residua
     code = _dtype_code(values.dtype)
     _check_params(values, weight, scales, biases, group_size, bits, "affine QMV")
     k = values.shape[-1]
-    n = weight.shape[0]
+    n = _code_shape(weight, bits)[0]
     lead = tuple(values.shape[:-1])
     x = values.reshape(-1, k).contiguous()
     m = x.shape[0]
@@ -121,7 +138,8 @@ def affine_qmv(values, weight, scales, biases, *, group_size=64, bits=4, residua
     L = _lib.lib()
     need = L.mt_affine_qmv_workspace_bytes(m, k, n, group_size, bits, 1)
     ws = workspace(values.device, need) if need else None
-    _lib.check(L.mt_affine_qmv(
+    fn = L.mt_affine_qmv_repacked if _repacked(w) else L.mt_affine_qmv
+    _lib.check(fn(
         x.data_ptr(), w.data_ptr(), s.data_ptr(), b.data_ptr(), _ptr(res), out.data_ptr(),
         m, k, n, group_size, bits, code, _ptr(ws), 0 if ws is None else ws.numel(),
         _stream_handle(values.device)))
@@ -143,7 +161,7 @@ def affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_s
         raise ValueError("affine SwiGLU requires matching gate/up weights and parameters")
     _check_params(values, gate_weight, gate_scales, gate_biases, group_size, bits, "affine SwiGLU")
     k = values.shape[-1]
-    n = gate_weight.shape[0]
+    n = _code_shape(gate_weight, bits)[0]
     lead = tuple(values.shape[:-1])
     x = values.reshape(-1, k).contiguous()
     m = x.shape[0]
@@ -156,7 +174,8 @@ def affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_s
     L = _lib.lib()
     need = L.mt_affine_qmv_workspace_bytes(m, k, n, group_size, bits, 2)
     ws = workspace(values.device, need) if need else None
-    _lib.check(L.mt_affine_swiglu(
+    fn = L.mt_affine_swiglu_repacked if _repacked(gw) else L.mt_affine_swiglu
+    _lib.check(fn(
         x.data_ptr(), gw.data_ptr(), gs.data_ptr(), gb.data_ptr(), uw.data_ptr(), us.data_ptr(),
         ub.data_ptr(), out.data_ptr(), m, k, n, group_size, bits, code, _ptr(ws),
         0 if ws is None else ws.numel(), _stream_handle(values.device)))
@@ -169,19 +188,21 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
     through the workspace), two launches above that.
 
     ``gate``/``up``/``down`` are ``(weight, scales, biases)`` triples; gate/up ``[I, H]``,
-    down ``[H, I]``. The hidden activation is rounded to the activation dtype between the two
+    down ``[H, I]``, all three in one code layout (MLX rows or ``affine_repack``'s). The hidden activation is rounded to the activation dtype between the two
     projections, as the reference executor does (``metile/backends/mlx_quantized.py:1829-1830``).
     """
     gw, gs, gb = gate
     uw, us, ub = up
     dw, ds, db = down
+    if not (_repacked(gw) == _repacked(uw) == _repacked(dw)):
+        raise ValueError("affine MLP weights must share one code layout")
     _require_device(values, gw, gs, gb, uw, us, ub, dw, ds, db, residual)
     code = _dtype_code(values.dtype)
     _check_params(values, gw, gs, gb, group_size, bits, "affine MLP gate")
     _check_params(values, uw, us, ub, group_size, bits, "affine MLP up")
     hdim = values.shape[-1]
-    idim = gw.shape[0]
-    if dw.shape[0] != hdim or dw.shape[1] * 32 // bits != idim:
+    idim = _code_shape(gw, bits)[0]
+    if _code_shape(dw, bits) != (hdim, idim):
         raise ValueError("affine MLP received incompatible down-projection parameters")
     if (tuple(ds.shape) != (hdim, idim // group_size) or tuple(db.shape) != tuple(ds.shape)
             or ds.dtype != values.dtype or db.dtype != values.dtype):
@@ -202,7 +223,8 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
     L = _lib.lib()
     need = L.mt_affine_mlp_workspace_bytes(m, hdim, idim, group_size, bits)
     ws = workspace(values.device, need)
-    _lib.check(L.mt_affine_mlp(
+    fn = L.mt_affine_mlp_repacked if _repacked(gw) else L.mt_affine_mlp
+    _lib.check(fn(
         x.data_ptr(), *[t.data_ptr() for t in tensors], _ptr(res), out.data_ptr(), m, hdim, idim,
         group_size, bits, code, ws.data_ptr(), ws.numel(), _stream_handle(values.device)))
     return out
@@ -223,6 +245,28 @@ def affine_dequantize(weight, scales, biases, *, group_size=64, bits=4):
     _lib.check(_lib.lib().mt_affine_dequantize(
         w.data_ptr(), s.data_ptr(), b.data_ptr(), out.data_ptr(), n, k, group_size, bits, code,
         _stream_handle(weight.device)))
+    return out
+
+
+def affine_repack(weight, *, bits=4):
+    """Step-major repack of MLX affine codes for the small-row kernels: the ``8*bits`` bytes
+    holding codes ``[64t, 64t + 64)`` of row ``n`` become ``packed[t, n]``, so the codes every
+    column of a strip needs for one K step are contiguous. Returns ``[K/64, N, 2*bits]`` words
+    of the input's dtype. A one-time cost (one read and one write of the codes); the kernels'
+    results over it equal those over the MLX rows bit for bit."""
+    _require_device(weight)
+    if bits not in (4, 8):
+        raise ValueError("affine repack supports 4- and 8-bit codes")
+    if weight.ndim != 2:
+        raise ValueError("expected packed weight and matching two-dimensional parameters")
+    n = weight.shape[0]
+    k = weight.shape[1] * 32 // bits
+    if n < 1 or k < 64 or k % 64:
+        raise ValueError("affine repack requires K to be a positive multiple of 64")
+    w = _as_u32(weight)
+    out = torch.empty(k // 64, n, 2 * bits, dtype=w.dtype, device=w.device)
+    _lib.check(_lib.lib().mt_affine_repack(w.data_ptr(), out.data_ptr(), n, k, bits,
+                                           _stream_handle(w.device)))
     return out
 
 
@@ -348,6 +392,44 @@ def mlx_affine_swiglu_qmv(values, gate_weight, gate_scales, gate_biases, up_weig
                          up_biases, group_size=group_size, bits=bits)
 
 
+def repack_mlx_affine_weight(weight, scales, biases, *, bits=4):
+    """Drop-in for ``repack_mlx_affine_weight`` (``metile/backends/mlx_quantized.py:754-774``)
+    with its guards: returns ``(packed, scales, biases)`` for ``mlx_affine_qmv_nax`` and
+    ``mlx_affine_swiglu_qmv_nax``. The reference repacks to the K-major nibble layout its NAX
+    kernels read (and transposes the scales); here ``packed`` is ``affine_repack``'s step-major
+    layout, which these kernels read, and the scales and biases keep their layout."""
+    if biases is None:
+        raise ValueError("native affine QMV requires affine biases")
+    if weight.ndim != 2 or scales.ndim != 2 or biases.shape != scales.shape:
+        raise ValueError("expected packed weight and matching two-dimensional parameters")
+    return affine_repack(weight, bits=bits), scales, biases
+
+
+def mlx_affine_qmv_nax(values, packed, scales, biases, *, output_features, group_size=64,
+                       bits=4, block=32):
+    """Drop-in for ``mlx_affine_qmv_nax`` (``metile/backends/mlx_quantized.py:777-797``): the
+    QMV over weights from ``repack_mlx_affine_weight``. ``block`` picks among the reference's
+    Metal schedules and is validated only."""
+    if block not in (32, 64, 128, 256):
+        raise ValueError("unsupported affine QMV schedule")
+    if packed.ndim != 3 or packed.shape[1] != output_features:
+        raise ValueError("expected repacked weights with output_features columns")
+    return affine_qmv(values, packed, scales, biases, group_size=group_size, bits=bits)
+
+
+def mlx_affine_swiglu_qmv_nax(values, gate_packed, gate_scales, gate_biases, up_packed,
+                              up_scales, up_biases, *, output_features, group_size=64, bits=4,
+                              block=32):
+    """Drop-in for ``mlx_affine_swiglu_qmv_nax`` (``metile/backends/mlx_quantized.py:800-831``):
+    the fused gate/up SwiGLU over weights from ``repack_mlx_affine_weight``."""
+    if block not in (32, 64, 128, 256):
+        raise ValueError("unsupported affine SwiGLU schedule")
+    if gate_packed.ndim != 3 or gate_packed.shape[1] != output_features:
+        raise ValueError("expected repacked weights with output_features columns")
+    return affine_swiglu(values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
+                         up_biases, group_size=group_size, bits=bits)
+
+
 def _fidelity_gate(result, reference, what):
     """Raise unless ``result`` passes the reference tuner's affine fidelity gate against the
     native composition (``metile/backends/mlx_quantized.py:1256-1272,1297``). The reference
@@ -362,21 +444,25 @@ def _fidelity_gate(result, reference, what):
 def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
                                up_scales, up_biases, *, group_size=64, bits=4):
     """Drop-in for ``mlx_affine_swiglu_executor`` (``metile/backends/mlx_quantized.py:1723``):
-    validates once, checks the kernel against the native composition on the sample (the
-    reference tuner's fidelity gate) and returns ``execute(values)`` bound to the weights."""
+    validates once, repacks the weights ahead of time (``affine_repack``, as the reference's
+    executor does for its repacked schedules, ``metile/backends/mlx_quantized.py:1082-1100``),
+    checks the kernel against the native composition on the sample (the reference tuner's
+    fidelity gate) and returns ``execute(values)`` bound to the repacked weights."""
     from .native import native_affine_swiglu
 
     _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                    up_biases, group_size, bits)
+    gate_packed = affine_repack(gate_weight, bits=bits)
+    up_packed = affine_repack(up_weight, bits=bits)
     _fidelity_gate(
-        affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+        affine_swiglu(sample_values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
                       up_biases, group_size=group_size, bits=bits),
         native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
                              up_scales, up_biases, group_size=group_size, bits=bits),
         "affine SwiGLU")
 
     def execute(values):
-        return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
+        return affine_swiglu(values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
                              up_biases, group_size=group_size, bits=bits)
 
     return execute
@@ -386,10 +472,12 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
                             up_scales, up_biases, down_weight, down_scales, down_biases,
                             sample_residual, *, group_size=64, bits=4):
     """Drop-in for ``mlx_affine_mlp_executor`` (``metile/backends/mlx_quantized.py:1770-1832``):
-    binds the SwiGLU executor (with its fidelity gate), runs the residual guards and the
-    residual stage's fidelity gate on the sample's hidden activation, and returns
-    ``execute(values, residual) = down(swiglu(values)) + residual``."""
-    from .native import native_affine_residual_qmv
+    runs every argument check, repacks the three weights ahead of time (``affine_repack``),
+    gates the SwiGLU stage and, on the sample's hidden activation, the residual stage against
+    the native compositions (the reference tuner's fidelity gate), and returns
+    ``execute(values, residual) = down(swiglu(values)) + residual`` over the repacked weights
+    (one C-ABI call)."""
+    from .native import native_affine_residual_qmv, native_affine_swiglu
 
     # Every argument check first (on a shape-only stand-in for the hidden activation), then
     # the kernels.
@@ -399,19 +487,20 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
                         dtype=sample_values.dtype, device="meta")
     mlx_affine_residual_qmv_guards(probe, down_weight, down_scales, down_biases, sample_residual,
                                    group_size=group_size, bits=bits)
-    swiglu = mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases,
-                                        up_weight, up_scales, up_biases, group_size=group_size,
-                                        bits=bits)
-    hidden = swiglu(sample_values)
+    gate = (affine_repack(gate_weight, bits=bits), gate_scales, gate_biases)
+    up = (affine_repack(up_weight, bits=bits), up_scales, up_biases)
+    down = (affine_repack(down_weight, bits=bits), down_scales, down_biases)
+    hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)
     _fidelity_gate(
-        affine_qmv(hidden, down_weight, down_scales, down_biases, group_size=group_size,
-                   bits=bits, residual=sample_residual),
+        hidden,
+        native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
+                             up_scales, up_biases, group_size=group_size, bits=bits),
+        "affine SwiGLU")
+    _fidelity_gate(
+        affine_qmv(hidden, *down, group_size=group_size, bits=bits, residual=sample_residual),
         native_affine_residual_qmv(hidden, down_weight, down_scales, down_biases,
                                    sample_residual, group_size=group_size, bits=bits),
         "affine residual QMV")
-    gate = (gate_weight, gate_scales, gate_biases)
-    up = (up_weight, up_scales, up_biases)
-    down = (down_weight, down_scales, down_biases)
 
     def execute(values, residual):
         return affine_mlp(values, gate, up, down, group_size=group_size, bits=bits,

@@ -125,6 +125,24 @@ def unpack_codes(w_q, bits: int) -> np.ndarray:
     return codes.reshape(w.shape[0], w.shape[1] * per_word)
 
 
+def repack_step_major(w_q, bits: int) -> np.ndarray:
+    """Step-major repack of MLX affine words ``[N, K*bits/32]`` into ``[K/64, N, 2*bits]``
+    words: chunk ``[t, n]`` holds the ``8*bits`` bytes of row ``n`` that carry codes
+    ``[64t, 64t + 64)``, unchanged. This is the layout the gfx950 small-row kernels read; it has
+    no counterpart in the reference, whose repack (``metile/backends/mlx_quantized.py:754-774``)
+    produces a K-major nibble layout for its NAX kernels. A pure reordering of whole 32-bit
+    words (a 64-code chunk is 2*bits words), written as a reshape and transpose.
+    """
+    if bits not in (4, 8):
+        raise ValueError("bits must be 4 or 8")
+    w = np.ascontiguousarray(np.asarray(w_q, dtype=np.uint32))
+    n, words = w.shape
+    chunk = 2 * bits  # words per 64 codes
+    if words % chunk:
+        raise ValueError("K must be a multiple of 64")
+    return np.ascontiguousarray(w.reshape(n, words // chunk, chunk).transpose(1, 0, 2))
+
+
 def dequantize(w_q, scales, biases, group_size: int, bits: int, dtype: str = "bf16") -> np.ndarray:
     """Exact fp32 dequantization ``w = q*s + b`` with per-(row, group) scale and bias.
 
@@ -352,6 +370,8 @@ def algorithmic_bytes_affine(m: int, k: int, n: int, bits: int, group_size: int,
 PINNED_BY = {
     "f32_to_bf16_bits": "exhaustive comparison with torch.bfloat16 casting on edge patterns",
     "pack_codes/unpack_codes": "hand-built words (0x76543210 -> 0..7), round trip (hypothesis)",
+    "repack_step_major": "hand-built rows of known codes land at [t, n]; brute-force index loop; "
+                         "the inverse transpose restores the words",
     "dequantize": "closed form (q - zero) * s, brute-force loop of kernels/affine_qmv.py:32-51",
     "affine_qmv": "reference KAT tests/test_affine_quantized.py:120-163 (seed 211), torch CPU",
     "silu_mul": "special cases g=0, g>>0, g<<0, and torch.nn.functional.silu",

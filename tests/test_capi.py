@@ -52,3 +52,17 @@ def test_workspace_sizes_are_row_independent_plans():
     assert 0 < w1 < w32 == w64
     assert lib.mt_affine_mlp_workspace_bytes(4, 1536, 8960, 64, 4) >= 4 * 8960 * 2
     assert lib.mt_affine_qmv_workspace_bytes(1, 100, 64, 64, 4, 1) == 0  # invalid K
+
+
+def test_repack_argument_checks_without_gpu():
+    lib = _lib.lib()
+    buf = ctypes.c_void_p(256)  # never dereferenced: every case fails validation first
+    assert lib.mt_affine_repack(buf, buf, 16, 128, 3, None) == _lib.MT_ERR_INVALID_ARGUMENT
+    assert "bits" in lib.mt_last_error().decode()
+    assert lib.mt_affine_repack(buf, buf, 16, 100, 4, None) == _lib.MT_ERR_INVALID_ARGUMENT
+    assert "multiple of 64" in lib.mt_last_error().decode()
+    assert lib.mt_affine_repack(None, buf, 16, 128, 4, None) == _lib.MT_ERR_INVALID_ARGUMENT
+    assert "null" in lib.mt_last_error().decode()
+    assert lib.mt_affine_repack(ctypes.c_void_p(264), buf, 16, 128, 4, None) == \
+        _lib.MT_ERR_INVALID_ARGUMENT
+    assert "aligned" in lib.mt_last_error().decode()

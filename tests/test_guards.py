@@ -147,3 +147,38 @@ def test_affine_matmul_guards():
         mt.mlx_affine_matmul(torch.zeros(2, 64, dtype=torch.bfloat16), aw)
     with pytest.raises(TypeError, match="float16 or bfloat16"):
         mt.mlx_affine_matmul(torch.zeros(2, 128, dtype=torch.float32), aw)
+
+
+def test_repack_guards():
+    """repack_mlx_affine_weight's guards (metile/backends/mlx_quantized.py:765-767)."""
+    w, s, b = _affine(64, 128)
+    with pytest.raises(ValueError, match="requires affine biases"):
+        mt.repack_mlx_affine_weight(w, s, None)
+    with pytest.raises(ValueError, match="matching two-dimensional parameters"):
+        mt.repack_mlx_affine_weight(w[0], s, b)
+    with pytest.raises(ValueError, match="matching two-dimensional parameters"):
+        mt.repack_mlx_affine_weight(w, s, b[:, :1])
+
+
+def test_nax_entries_validate_schedule_and_layout():
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    w, s, b = _affine(64, 128)
+    packed = torch.zeros(2, 64, 8, dtype=torch.int32)
+    with pytest.raises(ValueError, match="unsupported affine QMV schedule"):
+        mt.mlx_affine_qmv_nax(x, packed, s, b, output_features=64, block=48)
+    with pytest.raises(ValueError, match="repacked weights"):
+        mt.mlx_affine_qmv_nax(x, w, s, b, output_features=64)
+    with pytest.raises(ValueError, match="repacked weights"):
+        mt.mlx_affine_swiglu_qmv_nax(x, packed, s, b, packed, s, b, output_features=32)
+
+
+def test_mixed_code_layouts_are_rejected():
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    w, s, b = _affine(256, 128)
+    packed = torch.zeros(2, 256, 8, dtype=torch.int32)
+    dw, ds, db = _affine(128, 256)
+    with pytest.raises(ValueError):
+        mt.affine_swiglu(x, w, s, b, packed, s, b)
+    with pytest.raises(ValueError, match="one code layout"):
+        mt.affine_mlp(x, (w, s, b), (w, s, b), (torch.zeros(4, 128, 8, dtype=torch.int32), ds,
+                                                  db))

@@ -72,6 +72,36 @@ def test_pack_unpack_round_trip(bits, n, words, seed):
     np.testing.assert_array_equal(O.pack_codes(O.unpack_codes(raw, bits), bits), raw)
 
 
+# ---- step-major repack --------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_repack_puts_each_rows_64_codes_at_their_step(bits):
+    # row n holds code (n + k // 64) % 2^bits at k: the chunk [t, n] must unpack to n + t only
+    n, k = 5, 256
+    codes = (np.arange(n)[:, None] + (np.arange(k) // 64)[None, :]) % (1 << bits)
+    packed = O.repack_step_major(O.pack_codes(codes, bits), bits)
+    assert packed.shape == (k // 64, n, 2 * bits)
+    for t in range(k // 64):
+        chunk_codes = O.unpack_codes(packed[t], bits)  # [n, 64]
+        np.testing.assert_array_equal(chunk_codes, np.broadcast_to(
+            ((np.arange(n) + t) % (1 << bits))[:, None], (n, 64)))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_repack_matches_a_brute_force_index_loop_and_inverts(bits):
+    rng = np.random.default_rng(17)
+    n, k = 7, 192
+    w = rng.integers(0, 2**32, size=(n, k * bits // 32), dtype=np.uint64).astype(np.uint32)
+    packed = O.repack_step_major(w, bits)
+    chunk = 2 * bits
+    for t in range(k // 64):
+        for row in range(n):
+            for e in range(chunk):
+                assert packed[t, row, e] == w[row, t * chunk + e]
+    np.testing.assert_array_equal(packed.transpose(1, 0, 2).reshape(n, -1), w)
+
+
 # ---- dequantization -----------------------------------------------------------------------
 
 
