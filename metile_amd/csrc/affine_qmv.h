@@ -32,6 +32,8 @@ struct QmvParams {
   // 8 * bits, step stride N * 8 * bits; see launch_affine_repack).
   uint32_t col_stride;
   uint32_t step_stride;
+  int col_align;             // staged kernels: strip boundaries at multiples of this many
+                             // columns (1, or a 128-byte line of repacked codes)
 };
 
 // Step-major repack of MLX affine codes: the 8 * bits bytes of column n and K step t (codes

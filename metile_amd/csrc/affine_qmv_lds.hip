@@ -78,8 +78,11 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   const int j = lane & 31;
   const int h = lane >> 5;
   const int M = p.M, K = p.K, N = p.N;
-  const int col0 = (int)(((int64_t)strip * N) / p.strips);
-  const int width = (int)(((int64_t)(strip + 1) * N) / p.strips) - col0;
+  // Strip boundaries fall on multiples of p.col_align columns (whole cache lines of the
+  // repacked codes, so no line is fetched by two strips).
+  const int units = N / p.col_align;
+  const int col0 = (int)(((int64_t)strip * units) / p.strips) * p.col_align;
+  const int width = (int)(((int64_t)(strip + 1) * units) / p.strips) * p.col_align - col0;
   const int steps_total = K >> 6;
   const int s_beg = split * p.steps_per_split;
   const int s_end = min(steps_total, s_beg + p.steps_per_split);

@@ -230,9 +230,14 @@ void set_layout(mt::QmvParams& p, int layout, int bits) {
   if (layout == kLayoutStepMajor) {
     p.col_stride = 8u * (uint32_t)bits;
     p.step_stride = (uint32_t)p.N * 8u * (uint32_t)bits;
+    // A 128-byte line of repacked codes holds 128 / (8 bits) columns of one K step; strips
+    // that split a line would each fetch it (balanced SwiGLU strips: 1.18x the algorithmic
+    // bytes).
+    p.col_align = 16 / bits;
   } else {
     p.col_stride = (uint32_t)p.K * (uint32_t)bits / 8u;
     p.step_stride = 8u * (uint32_t)bits;
+    p.col_align = 1;
   }
 }
 
