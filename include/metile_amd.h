@@ -87,6 +87,19 @@ int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* bi
                          float* out, int N, int K, int group_size, int bits, int dtype,
                          void* stream);
 
+/* ---- affine group quantization (dense -> MLX affine format) ------------------------------- */
+
+/* w [N, K] 16-bit (dtype) -> w_q [N, K*bits/32], scales and biases [N, K/group_size] in the
+ * same dtype. Per group: scale = max((max - min) / (2^bits - 1), 1e-7) with the sign and
+ * edge rule that makes the extreme of larger magnitude exactly representable, bias = that
+ * extreme (or 0), codes = rint((w - bias) / scale) clamped to [0, 2^bits - 1], computed in fp32
+ * with the stored (rounded) scale and bias. Restates MLX's affine quantize (mx.quantize,
+ * mode="affine"), which the reference calls in metile/backends/mlx_compressed_down.py:41-48;
+ * bit parity with MLX itself is not verified (MLX is not available here). bits in {4, 8};
+ * group_size in {32, 64, 128} dividing K. */
+int mt_affine_quantize(const void* w, uint32_t* w_q, void* scales, void* biases, int N, int K,
+                       int group_size, int bits, int dtype, void* stream);
+
 /* ---- ahead-of-time repack for the small-row kernels --------------------------------------- */
 
 /* Step-major repack of MLX affine codes: the 8*bits bytes holding codes [64t, 64t + 64) of row

@@ -36,6 +36,7 @@ SIGNATURES = {
     "mt_affine_mlp": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                            _I, _P, _Z, _P]),
     "mt_affine_dequantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "mt_affine_quantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "mt_affine_repack": (_I, [_P, _P, _I, _I, _I, _P]),
     "mt_affine_qmv_repacked": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_affine_swiglu_repacked": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,

@@ -11,6 +11,7 @@
 #include "affine_qmv.h"
 #include "dense_qmv.h"
 #include "affine_gemm.h"
+#include "affine_quantize.h"
 #include "stream_read.h"
 
 namespace {
@@ -605,6 +606,29 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
                          up_biases, down_w, down_scales, down_biases, residual, y, M, H, I,
                          group_size, bits, dtype, workspace, workspace_bytes, stream,
                          kLayoutMlx);
+}
+
+int mt_affine_quantize(const void* w, uint32_t* w_q, void* scales, void* biases, int N, int K,
+                       int group_size, int bits, int dtype, void* stream) {
+  if (bits != 4 && bits != 8)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_quantize: bits must be 4 or 8");
+  if (dtype != MT_BF16 && dtype != MT_F16)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_quantize: dtype must be MT_BF16 or MT_F16");
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_quantize: group_size must be 32, 64 or 128");
+  if (N < 1 || K < group_size || K % group_size)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                "mt_affine_quantize: N must be positive and K a positive multiple of group_size");
+  if (!w || !w_q || !scales || !biases)
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_quantize: null pointer");
+  if ((size_t)N * K * 2 >= (1ull << 31))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_quantize: tensor larger than 2 GiB");
+  const hipError_t e = mt::launch_affine_quantize(
+      static_cast<const uint16_t*>(w), w_q, static_cast<uint16_t*>(scales),
+      static_cast<uint16_t*>(biases), N, K, group_size, bits, dtype,
+      static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "mt_affine_quantize");
+  return MT_OK;
 }
 
 int mt_affine_repack(const uint32_t* w_q, uint32_t* out, int N, int K, int bits, void* stream) {

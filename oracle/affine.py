@@ -143,6 +143,44 @@ def repack_step_major(w_q, bits: int) -> np.ndarray:
     return np.ascontiguousarray(w.reshape(n, words // chunk, chunk).transpose(1, 0, 2))
 
 
+def affine_quantize(w, group_size: int, bits: int, dtype: str = "bf16"):
+    """Affine group quantization of dense 16-bit weights ``[N, K]`` (storage of ``dtype``) into
+    ``(w_q, scales, biases)`` in the MLX affine format, all arithmetic in float32.
+
+    Restates MLX's published affine quantize (``mx.quantize(w, group_size, bits,
+    mode="affine")``, mlx 0.32, called by ``metile/backends/mlx_compressed_down.py:41-48``):
+    per group, ``scale = max((max - min) / (2^bits - 1), 1e-7)``, negated unless
+    ``|min| > |max|``; the extreme of larger magnitude (``edge``) is made exactly representable:
+    ``q0 = rint(edge / scale)``, and if ``q0 != 0`` then ``scale = edge / q0`` and
+    ``bias = edge``, else ``bias = 0``. Scale and bias are rounded to ``dtype``; the codes are
+    ``rint((w - bias) / scale)`` with the rounded values, clamped to ``[0, 2^bits - 1]``.
+    Parity with MLX itself is unpinned (MLX is not installed); the known answers and bounds in
+    ``PINNED_BY`` pin this restatement.
+    """
+    wf = to_f32(w, dtype)
+    n, k = wf.shape
+    if k % group_size:
+        raise ValueError("K must be a multiple of group_size")
+    g = wf.reshape(n, k // group_size, group_size)
+    bins = np.float32((1 << bits) - 1)
+    w_max = g.max(axis=-1)
+    w_min = g.min(axis=-1)
+    low = np.abs(w_min) > np.abs(w_max)
+    scale = np.maximum((w_max - w_min) / bins, np.float32(1e-7)).astype(np.float32)
+    scale = np.where(low, scale, -scale).astype(np.float32)
+    edge = np.where(low, w_min, w_max).astype(np.float32)
+    q0 = np.rint(edge / scale).astype(np.float32)
+    nonzero = q0 != 0
+    scale = np.where(nonzero, edge / np.where(nonzero, q0, np.float32(1)), scale)
+    bias = np.where(nonzero, edge, np.float32(0)).astype(np.float32)
+    s_store = from_f32(scale.astype(np.float32), dtype)
+    b_store = from_f32(bias, dtype)
+    s = to_f32(s_store, dtype)[..., None]
+    b = to_f32(b_store, dtype)[..., None]
+    codes = np.clip(np.rint((g - b) / s), 0, bins).astype(np.uint32).reshape(n, k)
+    return pack_codes(codes, bits), s_store, b_store
+
+
 def dequantize(w_q, scales, biases, group_size: int, bits: int, dtype: str = "bf16") -> np.ndarray:
     """Exact fp32 dequantization ``w = q*s + b`` with per-(row, group) scale and bias.
 
@@ -373,6 +411,9 @@ PINNED_BY = {
     "repack_step_major": "hand-built rows of known codes land at [t, n]; brute-force index loop; "
                          "the inverse transpose restores the words",
     "dequantize": "closed form (q - zero) * s, brute-force loop of kernels/affine_qmv.py:32-51",
+    "affine_quantize": "known answers (a 0..15 ramp -> scale -1, bias 15; its negation -> scale "
+                       "1, bias -15; constant and zero groups reproduced exactly); every element "
+                       "within half a step of its dequantized value; brute-force per-group loop",
     "affine_qmv": "reference KAT tests/test_affine_quantized.py:120-163 (seed 211), torch CPU",
     "silu_mul": "special cases g=0, g>>0, g<<0, and torch.nn.functional.silu",
     "affine_mlp": "composition of pinned parts; torch CPU end-to-end",

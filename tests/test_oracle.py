@@ -287,3 +287,78 @@ def test_tolerance_metric_catches_planted_mistakes():
 
 def test_algorithmic_bytes_config0():
     assert O.algorithmic_bytes_affine(1, 1536, 8960, 4, 64) == 7_762_432
+
+
+# ---- affine quantization --------------------------------------------------------------------
+
+
+def _group_row(values, group=32):
+    """One row holding ``values`` tiled to a group, as bf16 storage."""
+    v = np.resize(np.asarray(values, dtype=np.float32), group)
+    return O.from_f32(v[None, :], "bf16")
+
+
+def test_quantize_known_answer_ascending_ramp():
+    w = _group_row(np.arange(16, dtype=np.float32))
+    w_q, s, b = O.affine_quantize(w, 32, 4)
+    assert O.to_f32(s, "bf16")[0, 0] == -1.0 and O.to_f32(b, "bf16")[0, 0] == 15.0
+    codes = O.unpack_codes(w_q, 4)[0]
+    np.testing.assert_array_equal(codes, 15 - np.resize(np.arange(16), 32))
+    np.testing.assert_array_equal(O.dequantize(w_q, s, b, 32, 4), O.to_f32(w, "bf16"))
+
+
+def test_quantize_known_answer_negative_ramp():
+    w = _group_row(-np.arange(16, dtype=np.float32))
+    w_q, s, b = O.affine_quantize(w, 32, 4)
+    assert O.to_f32(s, "bf16")[0, 0] == 1.0 and O.to_f32(b, "bf16")[0, 0] == -15.0
+    np.testing.assert_array_equal(O.dequantize(w_q, s, b, 32, 4), O.to_f32(w, "bf16"))
+
+
+@pytest.mark.parametrize("c", [0.0, 0.375, -2.5])
+def test_quantize_constant_groups_are_exact(c):
+    w = _group_row([c])
+    for bits in (4, 8):
+        w_q, s, b = O.affine_quantize(w, 32, bits)
+        np.testing.assert_array_equal(O.unpack_codes(w_q, bits), 0)
+        np.testing.assert_array_equal(O.dequantize(w_q, s, b, 32, bits), O.to_f32(w, "bf16"))
+
+
+@pytest.mark.parametrize("bits,g,dtype", [(4, 64, "bf16"), (8, 32, "bf16"), (4, 128, "f16")])
+def test_quantize_reconstruction_and_brute_force(bits, g, dtype):
+    rng = np.random.default_rng(bits * 1000 + g)
+    w = O.from_f32((rng.standard_normal((6, 256)) * 0.02).astype(np.float32), dtype)
+    w_q, s, b = O.affine_quantize(w, g, bits, dtype)
+    wf = O.to_f32(w, dtype)
+    deq = O.dequantize(w_q, s, b, g, bits, dtype)
+    sf = np.repeat(np.abs(O.to_f32(s, dtype)), g, axis=1)
+    # half a quantization step, plus what the 16-bit rounding of scale and bias can add; a
+    # clamped code may be a full step off (the edge rule can round q0 away from the range, e.g.
+    # max = -min gives q0 = rint(-7.5) = -8 at 4 bits and the other extreme maps to 16)
+    ulp = 2.0 ** (-8 if dtype == "bf16" else -11)
+    bf = np.repeat(np.abs(O.to_f32(b, dtype)), g, axis=1)
+    extra = ((1 << bits) - 1) * sf * ulp + bf * ulp + 1e-12
+    codes_all = O.unpack_codes(w_q, bits)
+    inner = (codes_all > 0) & (codes_all < (1 << bits) - 1)
+    err = np.abs(deq - wf)
+    assert np.all(err[inner] <= (0.5 * sf + extra)[inner])
+    assert np.all(err <= sf + extra)
+    # brute force: the same rule written out per group with Python floats rounded to float32
+    f32 = np.float32
+    codes = O.unpack_codes(w_q, bits)
+    for r in range(wf.shape[0]):
+        for gi in range(wf.shape[1] // g):
+            grp = wf[r, gi * g:(gi + 1) * g]
+            hi, lo = f32(grp.max()), f32(grp.min())
+            low = abs(lo) > abs(hi)
+            sc = f32(max(f32(f32(hi - lo) / f32((1 << bits) - 1)), f32(1e-7)))
+            sc = sc if low else f32(-sc)
+            edge = lo if low else hi
+            q0 = f32(np.rint(f32(edge / sc)))
+            bias = f32(0)
+            if q0 != 0:
+                sc, bias = f32(edge / q0), edge
+            s16 = O.to_f32(O.from_f32(np.array([sc], f32), dtype), dtype)[0]
+            b16 = O.to_f32(O.from_f32(np.array([bias], f32), dtype), dtype)[0]
+            assert O.to_f32(s, dtype)[r, gi] == s16 and O.to_f32(b, dtype)[r, gi] == b16
+            want = [min(max(np.rint(f32(f32(v - b16) / s16)), 0), (1 << bits) - 1) for v in grp]
+            np.testing.assert_array_equal(codes[r, gi * g:(gi + 1) * g], want)
