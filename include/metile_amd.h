@@ -169,6 +169,65 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
                           int K, int N, int dtype, void* workspace, size_t workspace_bytes,
                           void* stream);
 
+/* ---- plans: the tuner's knobs ------------------------------------------------------------ */
+
+/* How one small-row dispatch runs: the kernel, the number of K splits, the number of column
+ * strips (workgroup columns; N/32 for the register kernel, N/32 to 2N/32 for the staged kernel)
+ * and the strips per workgroup (1 or 2, staged kernel only). */
+typedef enum mt_qmv_kernel { MT_QMV_STAGED = 1, MT_QMV_REGISTER = 2 } mt_qmv_kernel;
+typedef struct mt_qmv_plan {
+  int kernel;
+  int ksplit;
+  int strips;
+  int tiles;
+} mt_qmv_plan;
+
+/* How the prefill GEMM runs: output tiles of tile x tile (64 or 128) and K splits. */
+typedef struct mt_gemm_plan {
+  int tile;
+  int ksplit;
+} mt_gemm_plan;
+
+/* By default every call plans itself from its shape. A tuner lists the plans a shape can take,
+ * measures them and installs the fastest; calls of that shape then take the installed plan
+ * (results stay within the kernels' tolerance; summation order may change). Installed plans are
+ * per process and keyed by (rows of one dispatch rounded up to a power of two, K, N, group_size,
+ * bits, nproj, dtype); both code layouts take the installed plan, so that their results stay
+ * bit-identical. The workspace queries cover every installed plan. These
+ * functions are the analogue of the reference's tuned-config selection and its persistent
+ * decisions (metile/backends/mlx_quantized.py:1225-1253,1275-1336,1393-1483; config lattice
+ * MLXAffineSwiGLUConfig :61-67, MLXAffineResidualConfig :70-75, MLXAffineMatmulConfig
+ * metile/backends/mlx_affine.py:36-41 with _candidate_configs :157-166). Host-only: they touch
+ * no device.
+ *
+ * M is the rows of one dispatch (1..32, 1..16 for groups of 32; calls with more rows run
+ * dispatches of that many); nproj 1 (QMV) or 2 (SwiGLU).
+ * Within an MLP call, the gate/up dispatch is the nproj = 2 shape (K = H, N = I) and the down
+ * dispatch the nproj = 1 shape (K = I, N = H). */
+
+/* The plan a dispatch of this shape takes now (installed, else the planner's). */
+int mt_affine_qmv_plan(int M, int K, int N, int group_size, int bits, int nproj, int dtype,
+                       mt_qmv_plan* out);
+/* Every plan valid for dispatches of up to row_bucket(M) rows: writes up to `capacity` and
+ * returns how many there are (or a negative mt_status). */
+int mt_affine_qmv_plan_candidates(int M, int K, int N, int group_size, int bits, int nproj,
+                                  mt_qmv_plan* out, int capacity);
+/* Install `plan` for the shape (rejects a plan the kernels cannot run); NULL removes it. */
+int mt_affine_qmv_plan_set(int M, int K, int N, int group_size, int bits, int nproj, int dtype,
+                           const mt_qmv_plan* plan);
+/* The same three for the prefill GEMM (4-bit; M = rows of the call, bucketed likewise). */
+int mt_affine_gemm_plan(int M, int K, int N, int group_size, int dtype, mt_gemm_plan* out);
+int mt_affine_gemm_plan_candidates(int M, int K, int N, int group_size, mt_gemm_plan* out,
+                                   int capacity);
+int mt_affine_gemm_plan_set(int M, int K, int N, int group_size, int dtype,
+                            const mt_gemm_plan* plan);
+/* Remove every installed plan. */
+int mt_plans_clear(void);
+/* SHA-256 of the kernel and boundary sources this library was built from (hex): the part of a
+ * persistent tuning key that retires decisions when the kernels change, as the reference's
+ * source-hash keys do (metile/backends/mlx_quantized.py:1393-1427). */
+const char* mt_source_digest(void);
+
 /* ---- measurement -------------------------------------------------------------------------- */
 
 /* Reads `bytes` from `p` with `blocks` workgroups of 16-byte loads and writes one word per

@@ -20,9 +20,28 @@ MT_ERR_HIP = -3
 MT_BF16 = 0
 MT_F16 = 1
 
+MT_QMV_STAGED = 1
+MT_QMV_REGISTER = 2
+
+
+class QmvPlan(ctypes.Structure):
+    """``mt_qmv_plan``."""
+
+    _fields_ = [("kernel", ctypes.c_int), ("ksplit", ctypes.c_int), ("strips", ctypes.c_int),
+                ("tiles", ctypes.c_int)]
+
+
+class GemmPlan(ctypes.Structure):
+    """``mt_gemm_plan``."""
+
+    _fields_ = [("tile", ctypes.c_int), ("ksplit", ctypes.c_int)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _Z = ctypes.c_size_t
+_QP = ctypes.POINTER(QmvPlan)
+_GP = ctypes.POINTER(GemmPlan)
 
 # name -> (restype, argtypes); mirrors include/metile_amd.h exactly.
 SIGNATURES = {
@@ -49,6 +68,14 @@ SIGNATURES = {
     "mt_dense_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "mt_dense_swiglu": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_dense_residual_qmv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
+    "mt_affine_qmv_plan": (_I, [_I, _I, _I, _I, _I, _I, _I, _QP]),
+    "mt_affine_qmv_plan_candidates": (_I, [_I, _I, _I, _I, _I, _I, _QP, _I]),
+    "mt_affine_qmv_plan_set": (_I, [_I, _I, _I, _I, _I, _I, _I, _QP]),
+    "mt_affine_gemm_plan": (_I, [_I, _I, _I, _I, _I, _GP]),
+    "mt_affine_gemm_plan_candidates": (_I, [_I, _I, _I, _I, _GP, _I]),
+    "mt_affine_gemm_plan_set": (_I, [_I, _I, _I, _I, _I, _GP]),
+    "mt_plans_clear": (_I, []),
+    "mt_source_digest": (ctypes.c_char_p, []),
 }
 
 _lock = threading.Lock()

@@ -7,6 +7,7 @@ all sources; objects go to ``metile_amd/_build/`` and the shared library to
 
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -40,9 +41,21 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
-def _compile(src: Path) -> Path:
+def source_digest() -> str:
+    """SHA-256 over the compiler flags and every kernel, boundary and header source, in name
+    order: the library reports it (``mt_source_digest``) so that persistent tuning decisions
+    are keyed to the code they were measured on."""
+    h = hashlib.sha256(" ".join(HIP_FLAGS).encode())
+    for path in sorted([*sources(), *CSRC.glob("*.h"), *INCLUDE.glob("*.h")],
+                       key=lambda p: p.name):
+        h.update(path.name.encode() + b"\0" + path.read_bytes() + b"\0")
+    return h.hexdigest()
+
+
+def _compile(src: Path, digest: str) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-I{CSRC}", f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIP_FLAGS, f"-DMT_SOURCE_DIGEST=\"{digest}\"", f"-I{CSRC}", f"-I{INCLUDE}",
+           "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
@@ -57,8 +70,9 @@ def build(verbose: bool = False) -> Path:
     """Compile every HIP/C++ source and link ``libmetile_amd.so``; returns its path."""
     BUILD.mkdir(exist_ok=True)
     srcs = sources()
+    digest = source_digest()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
-        objs = list(pool.map(_compile, srcs))
+        objs = list(pool.map(lambda src: _compile(src, digest), srcs))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)

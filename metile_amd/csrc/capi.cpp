@@ -4,9 +4,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
+#include <shared_mutex>
 #include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "affine_qmv.h"
 #include "dense_qmv.h"
@@ -83,6 +88,9 @@ bool use_lds_path(int rows, int steps_per_split, int nproj, int group_size) {
 
 constexpr int kCus = 256;  // compute units of an MI355X
 
+// Largest K split the tuner's candidate lists go to.
+constexpr int kMaxCandidateSplits = 32;
+
 // Code ring depth of the staged kernel for a shape (the stage counts its launcher picks; the
 // 4-bit ring is six stages deep, or three when every wave has at most three K steps).
 int staged_ring(int bits, int nproj, int group_size) {
@@ -94,14 +102,18 @@ int staged_ring(int bits, int nproj, int group_size) {
 // Plan of one small-row call chunk of `rows` rows: the split plan, and for the staged kernel
 // a strip count that evens out the CUs. Its column strips need not be 32 wide: a workgroup
 // takes columns [s N / strips, (s + 1) N / strips) (16 to 32 of them; the MFMA tile masks
-// the rest). When the grid of 32-column strips is not a whole number of workgroups per CU,
-// take the smallest strip count that is, if it lowers the columns the busiest CU streams:
-// with N / 32 = 280 strips on 256 CUs, 24 CUs would otherwise stream two full strips and set
-// the kernel's time. Only grids that are resident at once (two eight-wave workgroups per CU)
-// are rebalanced: a grid of several rounds evens out as workgroups retire, and its narrower
-// strips measured slower. (Changing the K split instead also measured slower: every split
-// adds a partial-sum hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
-Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
+// the rest). The fused gate/up kernel at one or two rows, when there are more 32-column
+// strips than CUs, takes the smallest strip count that is a whole number of workgroups per CU,
+// if it lowers the columns the busiest CU streams: with N / 32 = 280 strips on 256 CUs, 24 CUs
+// would otherwise stream two full strips and set the kernel's time (SwiGLU 1536 -> 8960 at
+// M = 1: 512 strips 7.75 us, 280 strips 8.0 us). Elsewhere the narrower strips measured
+// slower: one projection of that shape (512 strips 5.86 us, 280 strips 5.60 us), four rows or
+// more (two-strip workgroups below), fewer strips than CUs (SwiGLU 896 -> 4864: 256 strips
+// 5.16 us, 152 strips 4.99 us). Only grids that are resident at once (two eight-wave
+// workgroups per CU) are rebalanced: a grid of several rounds evens out as workgroups
+// retire. (Changing the K split instead also measured slower: every split adds a partial-sum
+// hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
+Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   Plan plan = plan_split(K, N);
   if (group_size == 32) {
     // Two groups per K step: split K until the staged kernel's scale rows and LDS take it.
@@ -117,7 +129,11 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
     }
   }
   // Split K further where that puts the rows on the staged kernel (its activation staging
-  // holds M * steps_per_split * 8 chunks), at most to twice the planned split; and in grids of
+  // holds M * steps_per_split * 8 chunks), at most to twice the planned split, except for the
+  // fused gate/up kernel above 8 rows (there the register kernel unsplit measured faster:
+  // SwiGLU 2048 -> 8192 at M = 16, 9.5 us against 11.6 us for the staged kernel over two
+  // splits; one 8-bit projection 5120 -> 17408 at M = 16 is fastest staged over three); and in
+  // grids of
   // several rounds of workgroups anyway, until every wave's K steps fit its code ring (a ring
   // that refills costs more than the extra split: K = 5120, N = 17408 at 8 bits measured
   // 30.3 us with 3 splits against 32.7 us with 2). A forced METILE_AMD_KSPLIT is kept.
@@ -129,7 +145,8 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
       c.ksplit = (steps + c.steps_per_split - 1) / c.steps_per_split;
       return c;
     };
-    if (!mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 1)) {
+    if ((rows <= 8 || nproj == 1) &&
+        !mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 1)) {
       for (int ks = plan.ksplit + 1; ks <= 2 * plan.ksplit && ks <= steps; ++ks) {
         const Plan c = split_into(ks);
         if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size, 1)) {
@@ -153,7 +170,8 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   if (env && std::string(env) == "32") return plan;
   const long base = N / 32, ks = plan.ksplit;
   const long per_cu_base = (base * ks + kCus - 1) / kCus;  // workgroups on the busiest CU
-  for (long rounds = per_cu_base; rounds <= per_cu_base + 1; ++rounds) {
+  const bool rebalance = nproj == 2 && rows <= 2 && base * ks > kCus;
+  for (long rounds = per_cu_base; rebalance && rounds <= per_cu_base + 1; ++rounds) {
     if ((rounds * kCus) % ks) continue;
     const long strips = rounds * kCus / ks;
     if (strips <= base || strips > 2 * base || strips > kMaxStrips) continue;
@@ -165,13 +183,14 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
       break;
     }
   }
-  // Two strips per workgroup when the grid is two workgroups per CU and there are more than 8
-  // rows: the two strips then share one staging of the activations (half the activation
-  // reads through each CU's memory pipeline). At 8 rows or fewer that staging is small and
-  // the 16-wave workgroup measured slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us).
-  // METILE_AMD_TILES=1 or 2 overrides where the shape allows.
+  // Two strips per workgroup when the grid is one to two workgroups per CU and there are 4
+  // rows or more: the two strips then share one staging of the activations (half the
+  // activation reads through each CU's memory pipeline; SwiGLU 1536 -> 8960 at M = 8: 8.06 us
+  // against 8.45 us). At fewer rows that staging is small and the 16-wave workgroup measured
+  // slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us). METILE_AMD_TILES=1 or 2 overrides
+  // where the shape allows.
   const long wgs = (long)plan.strips * plan.ksplit;
-  int tiles = (rows > 8 && plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
+  int tiles = (rows >= 4 && plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
   if (const char* t = std::getenv("METILE_AMD_TILES")) {
     const int forced = std::atoi(t);
     if (forced == 1 || (forced == 2 && plan.strips % 2 == 0)) tiles = forced;
@@ -186,16 +205,174 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
 // staged kernel's largest row bucket).
 int row_chunk(int group_size) { return group_size == 32 ? mt::kQmvLdsMaxRows : kRowChunk; }
 
+// ---- installed plans -----------------------------------------------------------------------
+// A tuner measures the plans mt_affine_qmv_plan_candidates lists and installs the fastest for a
+// shape with mt_affine_qmv_plan_set; calls of that shape then take it instead of the planner's.
+// Keys hold the rows of one dispatch rounded up to a power of two (a plan is validated at the
+// bucket's largest row count, and every resource it needs grows with the rows), the shape and
+// the dtype. Both code layouts take the same plan, so that their results stay bit-identical.
+// The table is per process; lookups take a shared lock only once a plan has been installed.
+
+int row_bucket(int rows) {
+  int b = 1;
+  while (b < rows) b <<= 1;
+  return b;
+}
+
+struct PlanKey {
+  int op, rows, K, N, nproj, G, bits, dtype;
+  bool operator==(const PlanKey& o) const {
+    return op == o.op && rows == o.rows && K == o.K && N == o.N && nproj == o.nproj &&
+           G == o.G && bits == o.bits && dtype == o.dtype;
+  }
+};
+
+struct PlanKeyHash {
+  size_t operator()(const PlanKey& k) const {
+    uint64_t h = 1469598103934665603ull;
+    for (int v : {k.op, k.rows, k.K, k.N, k.nproj, k.G, k.bits, k.dtype}) {
+      h ^= (uint64_t)(uint32_t)v;
+      h *= 1099511628211ull;
+    }
+    return (size_t)h;
+  }
+};
+
+enum PlanOp : int { kOpQmv = 0, kOpGemm = 1 };
+
+std::shared_mutex g_plans_mu;
+std::unordered_map<PlanKey, mt_qmv_plan, PlanKeyHash> g_qmv_plans;
+std::unordered_map<PlanKey, mt_gemm_plan, PlanKeyHash> g_gemm_plans;
+std::atomic<int> g_plans_installed{0};
+
+PlanKey qmv_key(int rows, int K, int N, int nproj, int group_size, int bits, int dtype) {
+  return PlanKey{kOpQmv, row_bucket(rows), K, N, nproj, group_size, bits, dtype};
+}
+
+bool find_qmv_plan(const PlanKey& key, mt_qmv_plan* out) {
+  if (g_plans_installed.load(std::memory_order_acquire) == 0) return false;
+  std::shared_lock<std::shared_mutex> lock(g_plans_mu);
+  const auto it = g_qmv_plans.find(key);
+  if (it == g_qmv_plans.end()) return false;
+  *out = it->second;
+  return true;
+}
+
+Plan split_plan(int steps, int ksplit) {
+  Plan p{};
+  p.steps_per_split = (steps + ksplit - 1) / ksplit;
+  p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
+  return p;
+}
+
+Plan from_public(const mt_qmv_plan& q, int K) {
+  Plan p = split_plan(K / 64, q.ksplit);
+  p.strips = q.strips;
+  p.staged = q.kernel == MT_QMV_STAGED;
+  p.tiles = p.staged ? q.tiles : 1;
+  return p;
+}
+
+mt_qmv_plan to_public(const Plan& p) {
+  mt_qmv_plan q{};
+  q.kernel = p.staged ? MT_QMV_STAGED : MT_QMV_REGISTER;
+  q.ksplit = p.ksplit;
+  q.strips = p.strips;
+  q.tiles = p.staged ? p.tiles : 1;
+  return q;
+}
+
+// Why `q` cannot run dispatches of up to `rows` rows at this shape ("" when it can): the
+// register kernel covers 32-column strips of up to 32 rows and groups of 64 or more; the staged
+// kernel up to 16 rows, N / 32 to 2 N / 32 strips (16 to 32 columns each) in workgroups of one or
+// two strips, within its LDS; every split holds at most kMaxGroupsPerSplit - 1 groups.
+std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size,
+                             const mt_qmv_plan& q) {
+  const int steps = K / 64, base = N / 32;
+  if (q.kernel != MT_QMV_STAGED && q.kernel != MT_QMV_REGISTER) return "unknown kernel";
+  if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
+  const Plan p = split_plan(steps, q.ksplit);
+  if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
+  const int groups = group_size == 32 ? 2 * p.steps_per_split : p.steps_per_split;
+  if (groups > mt::kMaxGroupsPerSplit - 1) return "too many groups per split";
+  if (q.kernel == MT_QMV_REGISTER) {
+    if (group_size == 32) return "the register kernel takes groups of 64 or more";
+    if (rows > kRowChunk) return "more rows than the register kernel takes";
+    if (q.strips != base || q.tiles != 1)
+      return "the register kernel runs N/32 strips, one per workgroup";
+    return "";
+  }
+  if (rows > mt::kQmvLdsMaxRows) return "more rows than the staged kernel takes";
+  if (q.strips < base || q.strips > 2 * base || q.strips > kMaxStrips)
+    return "staged strips must be in N/32..2N/32";
+  if (q.tiles != 1 && q.tiles != 2) return "tiles must be 1 or 2";
+  if (q.strips % q.tiles) return "strips must be a multiple of tiles";
+  if (!mt::affine_qmv_lds_fits(rows, p.steps_per_split, nproj, group_size, q.tiles))
+    return "the staged kernel's LDS does not hold this split at these rows";
+  return "";
+}
+
+// The plan dispatches of `rows` rows take: the installed one for the shape, else the planner's.
+Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits, int dtype) {
+  mt_qmv_plan q;
+  if (find_qmv_plan(qmv_key(rows, K, N, nproj, group_size, bits, dtype), &q))
+    return from_public(q, K);
+  return planner_qmv(rows, K, N, nproj, group_size, bits);
+}
+
+// Staged strip counts worth measuring at a K split: N / 32, and the counts that put a whole
+// number of workgroups on every CU within one round above the busiest CU's share.
+std::vector<int> strip_options(int N, int ksplit) {
+  std::vector<int> out{N / 32};
+  const long base = N / 32, per_cu = (base * ksplit + kCus - 1) / kCus;
+  for (long rounds = per_cu; rounds <= per_cu + 1; ++rounds) {
+    if ((rounds * kCus) % ksplit) continue;
+    const long strips = rounds * kCus / ksplit;
+    if (strips <= base || strips > 2 * base || strips > kMaxStrips) continue;
+    bool seen = false;
+    for (int v : out) seen |= v == strips;
+    if (!seen) out.push_back((int)strips);
+  }
+  return out;
+}
+
+std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int group_size) {
+  std::vector<mt_qmv_plan> out;
+  const int steps = K / 64;
+  int last = 0;
+  for (int ks = 1; ks <= steps && ks <= kMaxCandidateSplits; ++ks) {
+    const Plan p = split_plan(steps, ks);
+    if (p.ksplit == last) continue;
+    last = p.ksplit;
+    const mt_qmv_plan reg{MT_QMV_REGISTER, p.ksplit, N / 32, 1};
+    if (qmv_plan_problem(rows, K, N, nproj, group_size, reg).empty()) out.push_back(reg);
+    for (int strips : strip_options(N, p.ksplit))
+      for (int tiles : {1, 2}) {
+        const mt_qmv_plan st{MT_QMV_STAGED, p.ksplit, strips, tiles};
+        if (qmv_plan_problem(rows, K, N, nproj, group_size, st).empty()) out.push_back(st);
+      }
+  }
+  return out;
+}
+
 size_t qmv_workspace(int M, int K, int N, int nproj, int group_size, int bits) {
-  // Row chunks and one remainder chunk may plan differently.
+  // Row chunks and one remainder chunk may plan differently, and so may each dtype: the size
+  // covers every plan a call of this shape can take.
   const int chunk = row_chunk(group_size);
   size_t need = 0;
   for (int rows : {M < chunk ? M : chunk, M % chunk}) {
     if (rows < 1) continue;
-    const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits);
-    if (plan.ksplit <= 1) continue;
-    const size_t b = kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
-    if (b > need) need = b;
+    std::vector<Plan> plans{planner_qmv(rows, K, N, nproj, group_size, bits)};
+    for (int dtype : {MT_BF16, MT_F16}) {
+      mt_qmv_plan q;
+      if (find_qmv_plan(qmv_key(rows, K, N, nproj, group_size, bits, dtype), &q))
+        plans.push_back(from_public(q, K));
+    }
+    for (const Plan& plan : plans) {
+      if (plan.ksplit <= 1) continue;
+      const size_t b = kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+      if (b > need) need = b;
+    }
   }
   return need;
 }
@@ -261,7 +438,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
   const int chunk = row_chunk(group_size);
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int rows = (M - r0) < chunk ? (M - r0) : chunk;
-    const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits);
+    const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits, dtype);
     if (group_size == 32 && !plan.staged)
       return fail(MT_ERR_INVALID_ARGUMENT,
                   std::string(op) + ": no staged plan fits groups of 32 at this shape");
@@ -364,7 +541,7 @@ struct GemmPlan {
   int steps_per_split;
 };
 
-GemmPlan plan_gemm(int M, int K, int N) {
+GemmPlan planner_gemm(int M, int K, int N) {
   GemmPlan g;
   const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
   const int t64 = ((M + 63) / 64) * ((N + 63) / 64);
@@ -388,10 +565,82 @@ GemmPlan plan_gemm(int M, int K, int N) {
   return g;
 }
 
-size_t gemm_workspace(int M, int K, int N) {
-  const GemmPlan g = plan_gemm(M, K, N);
-  if (g.ksplit <= 1) return 0;
-  return kCounterBytes + (size_t)g.ksplit * M * N * 4;
+int gemm_tiles(int M, int N, int tile) {
+  const int t = tile == 2 ? 128 : 64;
+  return ((M + t - 1) / t) * ((N + t - 1) / t);
+}
+
+PlanKey gemm_key(int M, int K, int N, int group_size, int dtype) {
+  return PlanKey{kOpGemm, row_bucket(M), K, N, 1, group_size, 4, dtype};
+}
+
+bool find_gemm_plan(const PlanKey& key, mt_gemm_plan* out) {
+  if (g_plans_installed.load(std::memory_order_acquire) == 0) return false;
+  std::shared_lock<std::shared_mutex> lock(g_plans_mu);
+  const auto it = g_gemm_plans.find(key);
+  if (it == g_gemm_plans.end()) return false;
+  *out = it->second;
+  return true;
+}
+
+// Why `q` cannot run the prefill GEMM at this shape for up to `M` rows ("" when it can): 64 x 64
+// (tile 64) or 128 x 128 (tile 128) output tiles, K split into equal-length splits, and with a
+// split one arrival counter per output tile.
+std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
+  const int steps = K / 64;
+  if (q.tile != 64 && q.tile != 128) return "tile must be 64 or 128";
+  if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
+  const Plan p = split_plan(steps, q.ksplit);
+  if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
+  if (q.ksplit > 1 && gemm_tiles(M, N, q.tile == 128 ? 2 : 1) > kMaxStrips)
+    return "too many output tiles to split K";
+  return "";
+}
+
+GemmPlan plan_gemm(int M, int K, int N, int group_size, int dtype) {
+  mt_gemm_plan q;
+  if (find_gemm_plan(gemm_key(M, K, N, group_size, dtype), &q)) {
+    GemmPlan g;
+    g.tile = q.tile == 128 ? 2 : 1;
+    g.tiles = gemm_tiles(M, N, g.tile);
+    const Plan p = split_plan(K / 64, q.ksplit);
+    g.ksplit = p.ksplit;
+    g.steps_per_split = p.steps_per_split;
+    return g;
+  }
+  return planner_gemm(M, K, N);
+}
+
+mt_gemm_plan gemm_to_public(const GemmPlan& g) {
+  return mt_gemm_plan{g.tile == 2 ? 128 : 64, g.ksplit};
+}
+
+std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
+  std::vector<mt_gemm_plan> out;
+  const int steps = K / 64;
+  for (int tile : {64, 128}) {
+    int last = 0;
+    for (int ks = 1; ks <= steps && ks <= kMaxCandidateSplits / 2; ++ks) {
+      const Plan p = split_plan(steps, ks);
+      if (p.ksplit == last) continue;
+      last = p.ksplit;
+      const mt_gemm_plan q{tile, p.ksplit};
+      if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
+    }
+  }
+  return out;
+}
+
+size_t gemm_workspace(int M, int K, int N, int group_size) {
+  size_t need = 0;
+  for (int dtype : {MT_BF16, MT_F16}) {
+    const GemmPlan g = plan_gemm(M, K, N, group_size, dtype);
+    if (g.ksplit > 1) {
+      const size_t b = kCounterBytes + (size_t)g.ksplit * M * N * 4;
+      if (b > need) need = b;
+    }
+  }
+  return need;
 }
 
 // ---- one-launch MLP plan ---------------------------------------------------------------
@@ -725,7 +974,7 @@ size_t mt_affine_gemm_workspace_bytes(int M, int K, int N, int group_size, int b
   if (check_affine("mt_affine_gemm_workspace_bytes", 1, K, N, group_size, bits, MT_BF16) ||
       M < 1 || group_size < 64)
     return 0;
-  return gemm_workspace(M, K, N);
+  return gemm_workspace(M, K, N, group_size);
 }
 
 int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const void* biases,
@@ -743,8 +992,8 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: tensor larger than 2 GiB");
   if (!x || !w_q || !scales || !biases || !y)
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm: null pointer");
-  const GemmPlan g = plan_gemm(M, K, N);
-  const size_t need = gemm_workspace(M, K, N);
+  const GemmPlan g = plan_gemm(M, K, N, group_size, dtype);
+  const size_t need = gemm_workspace(M, K, N, group_size);
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, "mt_affine_gemm: workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
@@ -769,6 +1018,123 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
   p.steps_per_split = g.steps_per_split;
   const hipError_t e = mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "mt_affine_gemm");
+  return MT_OK;
+}
+
+// ---- plans ------------------------------------------------------------------------------------
+
+#ifndef MT_SOURCE_DIGEST
+#define MT_SOURCE_DIGEST "unknown"
+#endif
+
+const char* mt_source_digest(void) { return MT_SOURCE_DIGEST; }
+
+static int check_qmv_plan_shape(const char* op, int M, int K, int N, int group_size, int bits,
+                                int nproj, int dtype) {
+  const int st = check_affine(op, M, K, N, group_size, bits, dtype);
+  if (st) return st;
+  if (nproj != 1 && nproj != 2)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": nproj must be 1 or 2");
+  if (M > row_chunk(group_size))
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": M is the rows of one dispatch, at most " +
+                    std::to_string(row_chunk(group_size)) + " at this group size");
+  return MT_OK;
+}
+
+int mt_affine_qmv_plan(int M, int K, int N, int group_size, int bits, int nproj, int dtype,
+                       mt_qmv_plan* out) {
+  const int st =
+      check_qmv_plan_shape("mt_affine_qmv_plan", M, K, N, group_size, bits, nproj, dtype);
+  if (st) return st;
+  if (!out) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_qmv_plan: null output");
+  *out = to_public(plan_qmv(M, K, N, nproj, group_size, bits, dtype));
+  return MT_OK;
+}
+
+int mt_affine_qmv_plan_candidates(int M, int K, int N, int group_size, int bits, int nproj,
+                                  mt_qmv_plan* out, int capacity) {
+  const int st = check_qmv_plan_shape("mt_affine_qmv_plan_candidates", M, K, N, group_size, bits,
+                                      nproj, MT_BF16);
+  if (st) return st;
+  if (capacity < 0 || (capacity > 0 && !out))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_qmv_plan_candidates: bad output buffer");
+  const std::vector<mt_qmv_plan> c = qmv_candidates(row_bucket(M), K, N, nproj, group_size);
+  for (int i = 0; i < (int)c.size() && i < capacity; ++i) out[i] = c[i];
+  return (int)c.size();
+}
+
+int mt_affine_qmv_plan_set(int M, int K, int N, int group_size, int bits, int nproj, int dtype,
+                           const mt_qmv_plan* plan) {
+  const int st =
+      check_qmv_plan_shape("mt_affine_qmv_plan_set", M, K, N, group_size, bits, nproj, dtype);
+  if (st) return st;
+  const PlanKey key = qmv_key(M, K, N, nproj, group_size, bits, dtype);
+  if (plan) {
+    const std::string why = qmv_plan_problem(key.rows, K, N, nproj, group_size, *plan);
+    if (!why.empty()) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_qmv_plan_set: " + why);
+  }
+  std::unique_lock<std::shared_mutex> lock(g_plans_mu);
+  if (plan) g_qmv_plans[key] = *plan;
+  else g_qmv_plans.erase(key);
+  g_plans_installed.store((int)(g_qmv_plans.size() + g_gemm_plans.size()),
+                          std::memory_order_release);
+  return MT_OK;
+}
+
+static int check_gemm_plan_shape(const char* op, int M, int K, int N, int group_size,
+                                 int dtype) {
+  const int st = check_affine(op, 1, K, N, group_size, 4, dtype);
+  if (st) return st;
+  if (M < 1) return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": M must be positive");
+  if (group_size < 64)
+    return fail(MT_ERR_INVALID_ARGUMENT,
+                std::string(op) + ": the prefill GEMM takes groups of 64 or more");
+  return MT_OK;
+}
+
+int mt_affine_gemm_plan(int M, int K, int N, int group_size, int dtype, mt_gemm_plan* out) {
+  const int st = check_gemm_plan_shape("mt_affine_gemm_plan", M, K, N, group_size, dtype);
+  if (st) return st;
+  if (!out) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm_plan: null output");
+  *out = gemm_to_public(plan_gemm(M, K, N, group_size, dtype));
+  return MT_OK;
+}
+
+int mt_affine_gemm_plan_candidates(int M, int K, int N, int group_size, mt_gemm_plan* out,
+                                   int capacity) {
+  const int st =
+      check_gemm_plan_shape("mt_affine_gemm_plan_candidates", M, K, N, group_size, MT_BF16);
+  if (st) return st;
+  if (capacity < 0 || (capacity > 0 && !out))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm_plan_candidates: bad output buffer");
+  const std::vector<mt_gemm_plan> c = gemm_candidates(row_bucket(M), K, N);
+  for (int i = 0; i < (int)c.size() && i < capacity; ++i) out[i] = c[i];
+  return (int)c.size();
+}
+
+int mt_affine_gemm_plan_set(int M, int K, int N, int group_size, int dtype,
+                            const mt_gemm_plan* plan) {
+  const int st = check_gemm_plan_shape("mt_affine_gemm_plan_set", M, K, N, group_size, dtype);
+  if (st) return st;
+  const PlanKey key = gemm_key(M, K, N, group_size, dtype);
+  if (plan) {
+    const std::string why = gemm_plan_problem(key.rows, K, N, *plan);
+    if (!why.empty()) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_gemm_plan_set: " + why);
+  }
+  std::unique_lock<std::shared_mutex> lock(g_plans_mu);
+  if (plan) g_gemm_plans[key] = *plan;
+  else g_gemm_plans.erase(key);
+  g_plans_installed.store((int)(g_qmv_plans.size() + g_gemm_plans.size()),
+                          std::memory_order_release);
+  return MT_OK;
+}
+
+int mt_plans_clear(void) {
+  std::unique_lock<std::shared_mutex> lock(g_plans_mu);
+  g_qmv_plans.clear();
+  g_gemm_plans.clear();
+  g_plans_installed.store(0, std::memory_order_release);
   return MT_OK;
 }
 

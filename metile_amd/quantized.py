@@ -3,9 +3,9 @@
 The public functions keep meTile's MLX-backend call surface
 (``metile/backends/mlx_quantized.py``): the same names, positional/keyword arguments,
 argument meaning and ``ValueError`` guards, but they take and return torch tensors on a ROCm
-device and always run the hand-written HIP kernels through the C ABI (there is no other code
-path to select, so the reference's autotune/fallback arguments are accepted and have no
-effect on the result).
+device and always run the hand-written HIP kernels through the C ABI. There is no fallback
+path: the reference's ``autotune`` arguments choose among this library's own plans for a shape
+(split-K, strips, kernel; ``metile_amd.tuning``), never another implementation.
 
 Tensor formats (MLX affine): ``weight`` uint32 (or int32 holding the same bits)
 ``[N, K*bits/32]``; ``scales``/``biases`` ``[N, K/group_size]`` in the activation dtype
@@ -23,6 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+from . import tuning as _tuning
 
 _DTYPES = {torch.bfloat16: _lib.MT_BF16, torch.float16: _lib.MT_F16}
 
@@ -32,6 +33,9 @@ _DTYPES = {torch.bfloat16: _lib.MT_BF16, torch.float16: _lib.MT_F16}
 
 _ws_lock = threading.RLock()
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Buffers replaced by a larger one stay allocated: a HIP graph captured earlier keeps their
+# address. Growth doubles, so the retired buffers never exceed the live one.
+_retired: list[torch.Tensor] = []
 
 
 def _stream_handle(device: torch.device) -> int:
@@ -42,14 +46,18 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Return a zero-initialised uint8 workspace of at least ``nbytes`` for the current stream.
 
     Calls on one stream are ordered, so they may share it; the kernels leave its counter
-    region zeroed after each call.
+    region zeroed after each call. A buffer that is outgrown is kept, not freed, so that graphs
+    captured over it stay valid.
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            _stream_handle(device))
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            size = max(nbytes, 1 << 20, 2 * buf.numel() if buf is not None else 0)
+            if buf is not None:
+                _retired.append(buf)
+            buf = torch.zeros(size, dtype=torch.uint8, device=device)
             _workspaces[key] = buf
         return buf
 
@@ -352,9 +360,13 @@ def mlx_affine_qmv(values, weight, scales, biases, *, group_size=64, bits=4, blo
 def mlx_affine_residual_qmv(values, weight, scales, biases, residual, *, group_size=64, bits=4,
                             autotune=True):
     """Drop-in for ``mlx_affine_residual_qmv`` with the reference's guards
-    (``metile/backends/mlx_quantized.py:1538-1568``)."""
+    (``metile/backends/mlx_quantized.py:1538-1568``). With ``autotune`` the first call of a
+    shape takes its tuned plan (``metile_amd.tuning``: cached, else measured once)."""
     mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual,
                                    group_size=group_size, bits=bits)
+    if autotune and values.numel():
+        _tuning.ensure_qmv_plans(values, (weight, scales, biases), group_size=group_size,
+                                 bits=bits)
     return affine_qmv(values, weight, scales, biases, group_size=group_size, bits=bits,
                       residual=residual)
 
@@ -374,9 +386,14 @@ def _swiglu_guards(values, gate_weight, gate_scales, gate_biases, up_weight, up_
 def mlx_affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                       up_biases, *, group_size=64, bits=4, autotune=True):
     """Drop-in for ``mlx_affine_swiglu`` with the reference's guards
-    (``metile/backends/mlx_quantized.py:1645-1670``)."""
+    (``metile/backends/mlx_quantized.py:1645-1670``). With ``autotune`` the first call of a
+    shape takes its tuned plan (``metile_amd.tuning``: cached, else measured once), as the
+    reference's tuned dispatch does (``:1671-1720``)."""
     _swiglu_guards(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                    up_biases, group_size, bits)
+    if autotune and values.numel():
+        _tuning.ensure_qmv_plans(values, (gate_weight, gate_scales, gate_biases, up_weight,
+                                          up_scales, up_biases), group_size=group_size, bits=bits)
     return affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                          up_biases, group_size=group_size, bits=bits)
 
@@ -442,10 +459,11 @@ def _fidelity_gate(result, reference, what):
 
 
 def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
-                               up_scales, up_biases, *, group_size=64, bits=4):
+                               up_scales, up_biases, *, group_size=64, bits=4, autotune=True):
     """Drop-in for ``mlx_affine_swiglu_executor`` (``metile/backends/mlx_quantized.py:1723``):
     validates once, repacks the weights ahead of time (``affine_repack``, as the reference's
     executor does for its repacked schedules, ``metile/backends/mlx_quantized.py:1082-1100``),
+    tunes the plan of the sample's shape (``metile_amd.tuning``; cached decisions are reused),
     checks the kernel against the native composition on the sample (the reference tuner's
     fidelity gate) and returns ``execute(values)`` bound to the repacked weights."""
     from .native import native_affine_swiglu
@@ -454,6 +472,10 @@ def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_bia
                    up_biases, group_size, bits)
     gate_packed = affine_repack(gate_weight, bits=bits)
     up_packed = affine_repack(up_weight, bits=bits)
+    if autotune:
+        _tuning.ensure_qmv_plans(sample_values, (gate_packed, gate_scales, gate_biases,
+                                                 up_packed, up_scales, up_biases),
+                                 group_size=group_size, bits=bits)
     _fidelity_gate(
         affine_swiglu(sample_values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
                       up_biases, group_size=group_size, bits=bits),
@@ -470,10 +492,11 @@ def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_bia
 
 def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
                             up_scales, up_biases, down_weight, down_scales, down_biases,
-                            sample_residual, *, group_size=64, bits=4):
+                            sample_residual, *, group_size=64, bits=4, autotune=True):
     """Drop-in for ``mlx_affine_mlp_executor`` (``metile/backends/mlx_quantized.py:1770-1832``):
     runs every argument check, repacks the three weights ahead of time (``affine_repack``),
-    gates the SwiGLU stage and, on the sample's hidden activation, the residual stage against
+    tunes the plans of both stages at the sample's shape (``metile_amd.tuning``), gates the
+    SwiGLU stage and, on the sample's hidden activation, the residual stage against
     the native compositions (the reference tuner's fidelity gate), and returns
     ``execute(values, residual) = down(swiglu(values)) + residual`` over the repacked weights
     (one C-ABI call)."""
@@ -490,7 +513,11 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
     gate = (affine_repack(gate_weight, bits=bits), gate_scales, gate_biases)
     up = (affine_repack(up_weight, bits=bits), up_scales, up_biases)
     down = (affine_repack(down_weight, bits=bits), down_scales, down_biases)
+    if autotune:
+        _tuning.ensure_qmv_plans(sample_values, (*gate, *up), group_size=group_size, bits=bits)
     hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)
+    if autotune:
+        _tuning.ensure_qmv_plans(hidden, down, group_size=group_size, bits=bits)
     _fidelity_gate(
         hidden,
         native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
@@ -530,7 +557,8 @@ def mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual, *, 
 
 def mlx_affine_matmul(values, weight, *, autotune=True):
     """Drop-in for ``mlx_affine_matmul`` (``metile/backends/mlx_affine.py:359-406``) with the
-    reference's guards. The reference's Metal path takes float16 only; the gfx950 GEMM also
+    reference's guards; with ``autotune`` the first call of a shape takes its tuned GEMM plan
+    (``metile_amd.tuning``), as the reference's tuned dispatch does (``:380-406``). The reference's Metal path takes float16 only; the gfx950 GEMM also
     takes bfloat16 (BASELINE config 4 is bf16), and any other dtype raises ``TypeError``."""
     if not isinstance(weight, AffineWeight):
         raise TypeError("weight must be an AffineWeight")
@@ -538,5 +566,8 @@ def mlx_affine_matmul(values, weight, *, autotune=True):
         raise ValueError("expected values[..., K] and a KxN affine weight")
     if values.dtype not in _DTYPES:
         raise TypeError("affine matmul requires float16 or bfloat16 activations")
+    if autotune and values.numel() and weight.bits == 4 and weight.group_size >= 64:
+        _tuning.ensure_gemm_plan(values, weight.native_weight, weight.native_scales,
+                                 weight.native_biases, group_size=weight.group_size)
     return affine_matmul(values, weight.native_weight, weight.native_scales,
                          weight.native_biases, group_size=weight.group_size, bits=weight.bits)

@@ -1,0 +1,598 @@
+"""Plan tuning with a persistent decision cache.
+
+Every C-ABI call plans itself from its shape (split-K, column strips, kernel). The planner's rules
+were measured at the BASELINE shapes; for any other shape this module measures the plans the
+library lists for it (``mt_affine_qmv_plan_candidates``, ``mt_affine_gemm_plan_candidates``) and
+installs the fastest (``mt_affine_*_plan_set``), so that later calls of that shape take it. The
+decision is written to a JSON cache keyed by everything that can change it, as the reference's
+tuner and cache do (``metile/runtime/cache.py:12-56``; keys ``mlx_quantized.py:1393-1449``;
+tournament ``metile/tuning/tournament.py:45-94``; selection ``mlx_quantized.py:1225-1253,1275-1336``).
+
+What differs from the reference, by design:
+
+* The baseline every candidate must beat is the planner's own plan (the reference's is MLX's
+  native kernel). A candidate replaces it only when it is faster by ``SWITCH_MARGIN``; within
+  ``TIE_TOLERANCE`` of the fastest the plan with the fewest workgroups wins (fewer partial sums),
+  the analogue of the reference's shortest-description tie break.
+* Candidates are timed as the hot path runs: each plan's dispatches are captured once in a HIP
+  graph over enough copies of the weights (``COLD_BYTES``, more than twice the 256 MB Infinity
+  Cache) that every dispatch streams its weights from HBM, and the graphs are replayed in a
+  rotating, alternately reversed order (``round_robin``), then the finalists head to head against
+  the baseline (``confirm_pairwise``).
+* Every candidate's result must pass the reference tuner's fidelity gate
+  (``affine_swiglu_compatible``) against the planner plan's result before it is timed.
+
+Environment: ``METILE_AMD_CACHE_DIR`` (cache directory), ``METILE_AMD_DISABLE_DISK_CACHE=1``
+(neither read nor write decisions), ``METILE_AMD_DISABLE_TUNING=1`` (never measure; cached
+decisions still apply).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import json
+import os
+import platform
+import statistics
+import tempfile
+import threading
+from contextlib import suppress
+from dataclasses import asdict, dataclass
+from pathlib import Path
+
+import torch
+
+from . import _lib
+
+TUNER_VERSION = 1
+SWITCH_MARGIN = 0.02
+TIE_TOLERANCE = 0.0025
+FINALIST_SLACK = 1.10
+ROUNDS = 7
+CONFIRM_ROUNDS = 15
+COLD_BYTES = 600 << 20
+MAX_COPIES = 256
+CACHE_FILE = "affine-plans-v1.json"
+
+_LAYOUT_MLX, _LAYOUT_REPACKED = 0, 1
+_KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register"}
+_KERNEL_CODES = {v: k for k, v in _KERNELS.items()}
+
+
+# ---- cache files (restating metile/runtime/cache.py:12-56) -------------------------------------
+
+
+def cache_root() -> Path:
+    """The cache directory (not created here): ``METILE_AMD_CACHE_DIR``, else
+    ``$XDG_CACHE_HOME/metile_amd``, else ``~/.cache/metile_amd`` (``~/Library/Caches`` on macOS)."""
+    override = os.environ.get("METILE_AMD_CACHE_DIR")
+    if override:
+        return Path(override).expanduser()
+    if platform.system() == "Darwin":
+        return Path.home() / "Library" / "Caches" / "metile_amd"
+    xdg = os.environ.get("XDG_CACHE_HOME")
+    return Path(xdg).expanduser() / "metile_amd" if xdg else Path.home() / ".cache" / "metile_amd"
+
+
+def cache_path() -> Path:
+    return cache_root() / CACHE_FILE
+
+
+def stable_digest(payload) -> str:
+    """SHA-256 of the canonical JSON of ``payload`` (key order and spacing do not matter)."""
+    text = json.dumps(payload, sort_keys=True, separators=(",", ":"), default=str)
+    return hashlib.sha256(text.encode()).hexdigest()
+
+
+def read_json(path: Path, default):
+    """The JSON at ``path``, or ``default`` when it is missing, unreadable or malformed."""
+    try:
+        with path.open(encoding="utf-8") as f:
+            return json.load(f)
+    except (OSError, ValueError, TypeError):
+        return default
+
+
+def atomic_write_json(path: Path, payload) -> None:
+    """Replace ``path`` with ``payload`` so that readers see the old or the new file, whole."""
+    path.parent.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix=f".{path.name}.", dir=path.parent)
+    try:
+        with os.fdopen(fd, "wb") as f:
+            f.write(json.dumps(payload, indent=2, sort_keys=True).encode() + b"\n")
+            f.flush()
+            os.fsync(f.fileno())
+        os.replace(tmp, path)
+    finally:
+        with suppress(FileNotFoundError):
+            os.unlink(tmp)
+
+
+def disk_cache_enabled() -> bool:
+    return os.environ.get("METILE_AMD_DISABLE_DISK_CACHE") != "1"
+
+
+def tuning_enabled() -> bool:
+    return os.environ.get("METILE_AMD_DISABLE_TUNING") != "1"
+
+
+def token_bucket(rows: int) -> int:
+    """Rows rounded up to a power of two (the library keys installed plans the same way)."""
+    return 1 << max(rows - 1, 0).bit_length()
+
+
+# ---- plans ---------------------------------------------------------------------------------------
+
+
+@dataclass(frozen=True)
+class QmvPlan:
+    """One small-row dispatch plan (``mt_qmv_plan``)."""
+
+    kernel: str  # "staged" or "register"
+    ksplit: int
+    strips: int
+    tiles: int = 1
+
+    def to_c(self) -> _lib.QmvPlan:
+        return _lib.QmvPlan(_KERNEL_CODES[self.kernel], self.ksplit, self.strips, self.tiles)
+
+    @classmethod
+    def from_c(cls, p) -> "QmvPlan":
+        return cls(_KERNELS[p.kernel], p.ksplit, p.strips, p.tiles)
+
+    @property
+    def workgroups(self) -> int:
+        return self.strips // self.tiles * self.ksplit
+
+
+@dataclass(frozen=True)
+class GemmPlan:
+    """One prefill GEMM plan (``mt_gemm_plan``)."""
+
+    tile: int
+    ksplit: int
+
+    def to_c(self) -> _lib.GemmPlan:
+        return _lib.GemmPlan(self.tile, self.ksplit)
+
+    @classmethod
+    def from_c(cls, p) -> "GemmPlan":
+        return cls(p.tile, p.ksplit)
+
+    def workgroups(self, rows: int, n: int) -> int:
+        return -(-rows // self.tile) * -(-n // self.tile) * self.ksplit
+
+
+def _dtype_code(dtype) -> int:
+    return {torch.bfloat16: _lib.MT_BF16, torch.float16: _lib.MT_F16}[dtype]
+
+
+def qmv_plan(rows, k, n, group_size, bits, nproj, dtype) -> QmvPlan:
+    """The plan a dispatch of ``rows`` rows takes now (installed, else the planner's)."""
+    out = _lib.QmvPlan()
+    _lib.check(_lib.lib().mt_affine_qmv_plan(rows, k, n, group_size, bits, nproj,
+                                             _dtype_code(dtype), ctypes.byref(out)))
+    return QmvPlan.from_c(out)
+
+
+def qmv_plan_candidates(rows, k, n, group_size, bits, nproj) -> list[QmvPlan]:
+    L = _lib.lib()
+    count = L.mt_affine_qmv_plan_candidates(rows, k, n, group_size, bits, nproj, None, 0)
+    if count < 0:
+        _lib.check(count)
+    buf = (_lib.QmvPlan * max(count, 1))()
+    count = L.mt_affine_qmv_plan_candidates(rows, k, n, group_size, bits, nproj, buf, count)
+    return [QmvPlan.from_c(buf[i]) for i in range(count)]
+
+
+def install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan) -> None:
+    """Install ``plan`` for the shape, both code layouts (``None`` restores the planner's)."""
+    c = None if plan is None else ctypes.byref(plan.to_c())
+    _lib.check(_lib.lib().mt_affine_qmv_plan_set(rows, k, n, group_size, bits, nproj,
+                                                 _dtype_code(dtype), c))
+
+
+def gemm_plan(rows, k, n, group_size, dtype) -> GemmPlan:
+    out = _lib.GemmPlan()
+    _lib.check(_lib.lib().mt_affine_gemm_plan(rows, k, n, group_size, _dtype_code(dtype),
+                                              ctypes.byref(out)))
+    return GemmPlan.from_c(out)
+
+
+def gemm_plan_candidates(rows, k, n, group_size) -> list[GemmPlan]:
+    L = _lib.lib()
+    count = L.mt_affine_gemm_plan_candidates(rows, k, n, group_size, None, 0)
+    if count < 0:
+        _lib.check(count)
+    buf = (_lib.GemmPlan * max(count, 1))()
+    count = L.mt_affine_gemm_plan_candidates(rows, k, n, group_size, buf, count)
+    return [GemmPlan.from_c(buf[i]) for i in range(count)]
+
+
+def install_gemm_plan(rows, k, n, group_size, dtype, plan) -> None:
+    c = None if plan is None else ctypes.byref(plan.to_c())
+    _lib.check(_lib.lib().mt_affine_gemm_plan_set(rows, k, n, group_size, _dtype_code(dtype), c))
+
+
+def clear_plans() -> None:
+    """Remove every installed plan and forget this process's decisions (the disk cache stays)."""
+    with _lock:
+        _lib.check(_lib.lib().mt_plans_clear())
+        _decided.clear()
+
+
+# ---- tournament (restating metile/tuning/tournament.py:45-94) ----------------------------------
+
+
+def round_robin(candidates, rounds, measure):
+    """``{key: [seconds, ...]}``: every candidate ``(key, runner)`` timed once per round, the
+    order rotated by one each round and reversed every other round, so that no candidate keeps
+    a position or a neighbour."""
+    candidates = list(candidates)
+    samples = {key: [] for key, _ in candidates}
+    for index in range(rounds):
+        shift = index % len(candidates) if candidates else 0
+        ordered = candidates[shift:] + candidates[:shift]
+        if index & 1:
+            ordered.reverse()
+        for key, runner in ordered:
+            samples[key].append(measure(runner))
+    return samples
+
+
+def confirm_pairwise(candidates, baseline, rounds, measure):
+    """``{key: seconds}``: each candidate timed alternately with ``baseline`` alone, ranked by
+    its median ratio to the baseline in that pairing (drift between pairings cancels), and
+    given back as that ratio times the median of the baseline's pairing medians."""
+    candidates = list(candidates)
+    base = next(c for c in candidates if c[0] == baseline)
+    others = [c for c in candidates if c[0] != baseline]
+    if not others:
+        return {baseline: statistics.median(round_robin([base], rounds, measure)[baseline])}
+    ratios, base_times = {}, []
+    for cand in others:
+        s = round_robin([base, cand], rounds, measure)
+        b = statistics.median(s[baseline])
+        base_times.append(b)
+        ratios[cand[0]] = statistics.median(s[cand[0]]) / b
+    reference = statistics.median(base_times)
+    out = {baseline: reference}
+    out.update({key: r * reference for key, r in ratios.items()})
+    return out
+
+
+def choose(timings, baseline, cost, *, margin=SWITCH_MARGIN, tie=TIE_TOLERANCE):
+    """The key to install: the fastest of the candidates that beat ``baseline`` by ``margin``
+    (within ``tie`` of the fastest, the lowest ``cost(key)``), else ``baseline``."""
+    limit = timings[baseline] * (1.0 - margin)
+    eligible = {k: t for k, t in timings.items() if k != baseline and t < limit}
+    if not eligible:
+        return baseline
+    fastest = min(eligible.values())
+    tied = [k for k, t in eligible.items() if t <= fastest * (1.0 + tie)]
+    return min(tied, key=lambda k: (cost(k), eligible[k]))
+
+
+# ---- measuring plans on the GPU -----------------------------------------------------------------
+
+_lock = threading.RLock()
+_decided: dict[tuple, object] = {}
+_identity: dict[int, dict] = {}
+_BASELINE = "planner"
+
+
+def _device_identity(device) -> dict:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _identity:
+        props = torch.cuda.get_device_properties(index)
+        _identity[index] = {
+            "architecture": getattr(props, "gcnArchName", ""),
+            "device": props.name,
+            "compute_units": props.multi_processor_count,
+            "library": _lib.lib().mt_source_digest().decode(),
+            "tuner_source": hashlib.sha256(Path(__file__).read_bytes()).hexdigest(),
+        }
+    return _identity[index]
+
+
+def _persistent_key(device, op, shape: dict, candidates) -> str:
+    return stable_digest({
+        **_device_identity(device),
+        "op": op,
+        **shape,
+        "candidates": [asdict(c) for c in candidates],
+        "tuner": TUNER_VERSION,
+        "switch_margin": SWITCH_MARGIN,
+        "cold_bytes": COLD_BYTES,
+    })
+
+
+def _read_decision(key, plan_type):
+    """(found, plan): ``plan`` is None when the planner's plan was kept."""
+    if not disk_cache_enabled():
+        return False, None
+    entry = read_json(cache_path(), {}).get(key)
+    if not isinstance(entry, dict) or "plan" not in entry:
+        return False, None
+    if entry["plan"] is None:
+        return True, None
+    try:
+        return True, plan_type(**entry["plan"])
+    except TypeError:
+        return False, None
+
+
+def _write_decision(key, plan, record) -> None:
+    if not disk_cache_enabled():
+        return
+    payload = read_json(cache_path(), {})
+    if not isinstance(payload, dict):
+        payload = {}
+    payload[key] = {"plan": None if plan is None else asdict(plan), **record}
+    atomic_write_json(cache_path(), payload)
+
+
+def _tensor_bytes(*tensors) -> int:
+    return sum(t.numel() * t.element_size() for t in tensors)
+
+
+def _copies(weight_bytes: int) -> int:
+    return max(2, min(MAX_COPIES, -(-COLD_BYTES // max(weight_bytes, 1))))
+
+
+class _Bench:
+    """Times dispatches replayed from HIP graphs on one side stream; owns its workspace (grown
+    before any capture, so every graph keeps a valid pointer)."""
+
+    def __init__(self, device, workspace_bytes):
+        self.device = device
+        self.ws = torch.zeros(max(workspace_bytes, 1 << 16), dtype=torch.uint8, device=device)
+        self.stream = torch.cuda.Stream(device)
+        # inputs, weight copies and the workspace were written on the caller's stream
+        self.stream.wait_stream(torch.cuda.current_stream(device))
+        self.graphs = []
+
+    def capture(self, body):
+        with torch.cuda.stream(self.stream):
+            body()  # eager run first: the dispatch is checked outside capture
+            self.stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=self.stream):
+                body()
+        self.graphs.append(g)
+        return g
+
+    def measure(self, graph):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(self.stream):
+            start.record(self.stream)
+            graph.replay()
+            end.record(self.stream)
+        end.synchronize()
+        return start.elapsed_time(end) * 1e-3
+
+    def close(self):
+        self.graphs.clear()
+        torch.cuda.synchronize(self.device)
+
+
+def _tournament(bench, graphs, copies, cost):
+    """Seconds per dispatch of each key of ``graphs`` (``{key: graph}``), and the key chosen."""
+    measure = bench.measure
+    entries = list(graphs.items())
+    for _, g in entries:  # one untimed replay each: clocks and caches in the steady state
+        measure(g)
+    provisional = {k: statistics.median(v) for k, v in round_robin(entries, ROUNDS, measure).items()}
+    best = min(provisional.values())
+    alternatives = [k for k in provisional if k != _BASELINE]
+    fastest_alt = min(alternatives, key=provisional.__getitem__) if alternatives else None
+    finalists = [(k, g) for k, g in entries
+                 if provisional[k] <= best * FINALIST_SLACK or k in (_BASELINE, fastest_alt)]
+    timings = confirm_pairwise(finalists, _BASELINE, CONFIRM_ROUNDS, measure)
+    timings = {k: t / copies for k, t in timings.items()}
+    return timings, choose(timings, _BASELINE, cost)
+
+
+def _gate(result, reference, what):
+    from .fidelity import affine_swiglu_compatible
+
+    if not affine_swiglu_compatible(result, reference):
+        raise RuntimeError(f"{what}: a plan failed the fidelity gate against the planner's plan")
+
+
+def _tune_qmv_dispatch(values, weights, group_size, bits, layout):
+    """Measure every plan of one dispatch shape (``values`` rows <= one dispatch) and return
+    ``(plan or None, record)``."""
+    from .quantized import _as_u32
+
+    L = _lib.lib()
+    nproj = len(weights) // 3
+    rows, k = values.shape
+    tensors = [_as_u32(t) if i % 3 == 0 else t.contiguous() for i, t in enumerate(weights)]
+    n = (tensors[0].shape[1] if layout == _LAYOUT_REPACKED else tensors[0].shape[0])
+    dtype = values.dtype
+    code = _dtype_code(dtype)
+    candidates = qmv_plan_candidates(rows, k, n, group_size, bits, nproj)
+    copies = _copies(_tensor_bytes(*tensors))
+    rotation = [tensors] + [[t.clone() for t in tensors] for _ in range(copies - 1)]
+    fn = ((L.mt_affine_qmv_repacked if layout == _LAYOUT_REPACKED else L.mt_affine_qmv)
+          if nproj == 1 else
+          (L.mt_affine_swiglu_repacked if layout == _LAYOUT_REPACKED else L.mt_affine_swiglu))
+    need = 0
+    for plan in [None, *candidates]:
+        install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan)
+        need = max(need, L.mt_affine_qmv_workspace_bytes(rows, k, n, group_size, bits, nproj))
+    install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, None)
+    bench = _Bench(values.device, need)
+    x = values.contiguous()
+    outs = [torch.empty(rows, n, dtype=dtype, device=values.device) for _ in range(copies)]
+
+    def body():
+        stream = torch.cuda.current_stream(values.device).cuda_stream
+        for ts, out in zip(rotation, outs):
+            ptrs = [t.data_ptr() for t in ts]
+            if nproj == 1:
+                args = (x.data_ptr(), *ptrs, None, out.data_ptr())
+            else:
+                args = (x.data_ptr(), *ptrs, out.data_ptr())
+            _lib.check(fn(*args, rows, k, n, group_size, bits, code, bench.ws.data_ptr(),
+                          bench.ws.numel(), stream))
+
+    graphs, reference = {}, None
+    try:
+        for key, plan in [(_BASELINE, None), *[(c, c) for c in candidates]]:
+            install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan)
+            graphs[key] = bench.capture(body)
+            bench.stream.synchronize()
+            if reference is None:
+                reference = outs[0].clone()
+            else:
+                _gate(outs[0], reference, "affine plan tuning")
+        install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, None)
+        timings, chosen = _tournament(bench, graphs, copies,
+                                      lambda key: -1 if key == _BASELINE else key.workgroups)
+    finally:
+        install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, None)
+        bench.close()
+    planner = qmv_plan(rows, k, n, group_size, bits, nproj, dtype)
+    plan = None if chosen == _BASELINE else chosen
+    record = {
+        "planner": asdict(planner),
+        "planner_us": round(timings[_BASELINE] * 1e6, 3),
+        "chosen_us": round(timings[chosen] * 1e6, 3),
+        "copies": copies,
+    }
+    return plan, record
+
+
+def _qmv_shape(rows, k, n, group_size, bits, nproj, dtype) -> dict:
+    return {"rows": token_bucket(rows), "input_features": k, "output_features": n,
+            "group_size": group_size, "bits": bits, "nproj": nproj, "dtype": str(dtype)}
+
+
+def dispatch_rows(rows: int, group_size: int) -> list[int]:
+    """Rows of the dispatches a call of ``rows`` rows makes (32 at a time, 16 for groups of
+    32), distinct buckets only."""
+    chunk = 16 if group_size == 32 else 32
+    out = []
+    for r in (min(rows, chunk), rows % chunk if rows > chunk else 0):
+        if r and token_bucket(r) not in {token_bucket(v) for v in out}:
+            out.append(r)
+    return out
+
+
+def ensure_qmv_plans(values, weights, *, group_size, bits, autotune=True, retune=False):
+    """Make the dispatches of ``values`` (any leading shape) over ``weights`` take their tuned
+    plans: ``weights`` is ``(w, scales, biases)`` (QMV) or the gate triple then the up triple
+    (SwiGLU), in MLX or repacked layout (measured in the layout given; the decision applies to
+    both). Per dispatch shape: this process's decision, else the disk cache's, else
+    (``autotune`` and tuning enabled, outside graph capture) a measurement, which is then
+    cached. Returns ``{rows: plan or None}`` (None: the planner's plan)."""
+    from .quantized import _repacked
+
+    nproj = len(weights) // 3
+    layout = _LAYOUT_REPACKED if _repacked(weights[0]) else _LAYOUT_MLX
+    k = values.shape[-1]
+    n = weights[0].shape[1] if layout == _LAYOUT_REPACKED else weights[0].shape[0]
+    x = values.reshape(-1, k)
+    out = {}
+    with _lock:
+        for rows in dispatch_rows(x.shape[0], group_size):
+            mem = ("qmv", values.device.index, token_bucket(rows), k, n, group_size, bits, nproj,
+                   values.dtype)
+            if mem in _decided and not retune:
+                out[rows] = _decided[mem]
+                continue
+            candidates = qmv_plan_candidates(rows, k, n, group_size, bits, nproj)
+            shape = _qmv_shape(rows, k, n, group_size, bits, nproj, values.dtype)
+            key = _persistent_key(values.device, "affine_qmv", shape, candidates)
+            found, plan = (False, None) if retune else _read_decision(key, QmvPlan)
+            if not found:
+                if (not autotune or not tuning_enabled()
+                        or torch.cuda.is_current_stream_capturing()):
+                    out[rows] = None
+                    continue  # not decided: the planner's plan, and measure another time
+                plan, record = _tune_qmv_dispatch(x[:rows], weights, group_size, bits, layout)
+                _write_decision(key, plan, {"op": "affine_qmv", **shape, **record})
+            install_qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype, plan)
+            _decided[mem] = plan
+            out[rows] = plan
+    return out
+
+
+def _tune_gemm(values, weight, scales, biases, group_size):
+    L = _lib.lib()
+    from .quantized import _as_u32
+
+    rows, k = values.shape
+    w, s, b = _as_u32(weight), scales.contiguous(), biases.contiguous()
+    n = w.shape[0]
+    dtype = values.dtype
+    code = _dtype_code(dtype)
+    candidates = gemm_plan_candidates(rows, k, n, group_size)
+    copies = _copies(_tensor_bytes(w, s, b))
+    rotation = [(w, s, b)] + [(w.clone(), s.clone(), b.clone()) for _ in range(copies - 1)]
+    need = 0
+    for plan in [None, *candidates]:
+        install_gemm_plan(rows, k, n, group_size, dtype, plan)
+        need = max(need, L.mt_affine_gemm_workspace_bytes(rows, k, n, group_size, 4))
+    install_gemm_plan(rows, k, n, group_size, dtype, None)
+    bench = _Bench(values.device, need)
+    x = values.contiguous()
+    outs = [torch.empty(rows, n, dtype=dtype, device=values.device) for _ in range(copies)]
+
+    def body():
+        stream = torch.cuda.current_stream(values.device).cuda_stream
+        for (ww, ss, bb), out in zip(rotation, outs):
+            _lib.check(L.mt_affine_gemm(x.data_ptr(), ww.data_ptr(), ss.data_ptr(), bb.data_ptr(),
+                                        out.data_ptr(), rows, k, n, group_size, 4, code,
+                                        bench.ws.data_ptr(), bench.ws.numel(), stream))
+
+    graphs, reference = {}, None
+    try:
+        for key, plan in [(_BASELINE, None), *[(c, c) for c in candidates]]:
+            install_gemm_plan(rows, k, n, group_size, dtype, plan)
+            graphs[key] = bench.capture(body)
+            bench.stream.synchronize()
+            if reference is None:
+                reference = outs[0].clone()
+            else:
+                _gate(outs[0], reference, "affine matmul plan tuning")
+        install_gemm_plan(rows, k, n, group_size, dtype, None)
+        timings, chosen = _tournament(
+            bench, graphs, copies,
+            lambda key: -1 if key == _BASELINE else key.workgroups(rows, n))
+    finally:
+        install_gemm_plan(rows, k, n, group_size, dtype, None)
+        bench.close()
+    planner = gemm_plan(rows, k, n, group_size, dtype)
+    plan = None if chosen == _BASELINE else chosen
+    return plan, {"planner": asdict(planner), "planner_us": round(timings[_BASELINE] * 1e6, 3),
+                  "chosen_us": round(timings[chosen] * 1e6, 3), "copies": copies}
+
+
+def ensure_gemm_plan(values, weight, scales, biases, *, group_size, autotune=True, retune=False):
+    """``ensure_qmv_plans`` for the prefill GEMM (4-bit codes in MLX layout)."""
+    k = values.shape[-1]
+    x = values.reshape(-1, k)
+    rows = x.shape[0]
+    n = weight.shape[0]
+    with _lock:
+        mem = ("gemm", values.device.index, token_bucket(rows), k, n, group_size, values.dtype)
+        if mem in _decided and not retune:
+            return _decided[mem]
+        candidates = gemm_plan_candidates(rows, k, n, group_size)
+        shape = {"rows": token_bucket(rows), "input_features": k, "output_features": n,
+                 "group_size": group_size, "bits": 4, "dtype": str(values.dtype)}
+        key = _persistent_key(values.device, "affine_matmul", shape, candidates)
+        found, plan = (False, None) if retune else _read_decision(key, GemmPlan)
+        if not found:
+            if not autotune or not tuning_enabled() or torch.cuda.is_current_stream_capturing():
+                return None
+            plan, record = _tune_gemm(x, weight, scales, biases, group_size)
+            _write_decision(key, plan, {"op": "affine_matmul", **shape, **record})
+        install_gemm_plan(rows, k, n, group_size, values.dtype, plan)
+        _decided[mem] = plan
+        return plan

@@ -1,0 +1,256 @@
+"""The tuner's host side, no GPU: the decision cache files and keys, the tournament's order and
+arithmetic, the selection rule, and the plan table of the C ABI (candidate lists, validation,
+installation, bucketing, workspace sizes), which is host-only code.
+
+The cache and tournament restate ``metile/runtime/cache.py:12-56`` and
+``metile/tuning/tournament.py:45-94``; the selection rule is this build's (a margin over the
+planner's plan, ties to the fewest workgroups)."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import pytest
+
+import metile_amd._lib as L
+from metile_amd import build, tuning
+from metile_amd.tuning import GemmPlan, QmvPlan
+
+
+# ---- cache files ---------------------------------------------------------------------------------
+
+
+def test_cache_root_precedence(monkeypatch, tmp_path):
+    monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path / "a"))
+    monkeypatch.setenv("XDG_CACHE_HOME", str(tmp_path / "x"))
+    assert tuning.cache_root() == tmp_path / "a"
+    monkeypatch.delenv("METILE_AMD_CACHE_DIR")
+    assert tuning.cache_root() == tmp_path / "x" / "metile_amd"
+    monkeypatch.delenv("XDG_CACHE_HOME")
+    assert tuning.cache_root().parts[-2:] == (".cache", "metile_amd")
+
+
+def test_stable_digest_ignores_key_order_and_sees_values():
+    a = tuning.stable_digest({"x": 1, "y": [1, 2], "z": {"b": 2, "a": 1}})
+    b = tuning.stable_digest({"z": {"a": 1, "b": 2}, "y": [1, 2], "x": 1})
+    assert a == b and len(a) == 64
+    assert a != tuning.stable_digest({"x": 1, "y": [2, 1], "z": {"b": 2, "a": 1}})
+
+
+def test_json_round_trip_and_unreadable_files(tmp_path):
+    path = tmp_path / "d" / "c.json"
+    assert tuning.read_json(path, {"missing": True}) == {"missing": True}
+    tuning.atomic_write_json(path, {"k": {"plan": None}})
+    assert tuning.read_json(path, {}) == {"k": {"plan": None}}
+    assert os.listdir(path.parent) == ["c.json"]  # no temporary file left behind
+    path.write_text("{not json")
+    assert tuning.read_json(path, "default") == "default"
+
+
+def test_decisions_round_trip_through_the_cache(monkeypatch, tmp_path):
+    monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
+    plan = QmvPlan("staged", 3, 544, 1)
+    tuning._write_decision("k1", plan, {"planner_us": 9.0})
+    tuning._write_decision("k2", None, {"planner_us": 5.0})
+    assert tuning._read_decision("k1", QmvPlan) == (True, plan)
+    assert tuning._read_decision("k2", QmvPlan) == (True, None)
+    assert tuning._read_decision("k3", QmvPlan) == (False, None)
+    data = json.loads(tuning.cache_path().read_text())
+    data["k4"] = {"plan": {"tile": 64}}  # malformed: missing a field
+    tuning.atomic_write_json(tuning.cache_path(), data)
+    assert tuning._read_decision("k4", GemmPlan) == (False, None)
+    monkeypatch.setenv("METILE_AMD_DISABLE_DISK_CACHE", "1")
+    assert tuning._read_decision("k1", QmvPlan) == (False, None)
+    tuning._write_decision("k5", plan, {})
+    monkeypatch.delenv("METILE_AMD_DISABLE_DISK_CACHE")
+    assert tuning._read_decision("k5", QmvPlan) == (False, None)
+
+
+def test_token_bucket_and_dispatch_rows():
+    assert [tuning.token_bucket(r) for r in (1, 2, 3, 5, 8, 9, 17, 32)] == [1, 2, 4, 8, 8, 16, 32,
+                                                                           32]
+    assert tuning.dispatch_rows(1, 64) == [1]
+    assert tuning.dispatch_rows(32, 64) == [32]
+    assert tuning.dispatch_rows(64, 64) == [32]
+    assert tuning.dispatch_rows(70, 64) == [32, 6]
+    assert tuning.dispatch_rows(20, 32) == [16, 4]
+    assert tuning.dispatch_rows(48, 32) == [16]
+
+
+# ---- tournament and selection --------------------------------------------------------------------
+
+
+def test_round_robin_rotates_and_reverses():
+    order = []
+    cands = [("a", "a"), ("b", "b"), ("c", "c")]
+    samples = tuning.round_robin(cands, 4, lambda r: order.append(r) or len(order))
+    assert order == ["a", "b", "c",  # shift 0
+                     "a", "c", "b",  # shift 1 (b c a), reversed
+                     "c", "a", "b",  # shift 2
+                     "c", "b", "a"]  # shift 0, reversed
+    assert {k: len(v) for k, v in samples.items()} == {"a": 4, "b": 4, "c": 4}
+
+
+def test_confirm_pairwise_rebuilds_times_from_ratios():
+    # each pairing drifts by a different factor; the ratios cancel it
+    drift = iter([1.0, 1.0, 1.0, 1.0, 2.0, 2.0, 2.0, 2.0])
+    times = {"base": 10.0, "x": 8.0, "y": 12.0}
+    got = tuning.confirm_pairwise([("base", "base"), ("x", "x"), ("y", "y")], "base", 2,
+                                  lambda r: times[r] * next(drift))
+    assert got["base"] == pytest.approx(15.0)  # median of the pairings' baselines (10, 20)
+    assert got["x"] == pytest.approx(0.8 * 15.0)
+    assert got["y"] == pytest.approx(1.2 * 15.0)
+
+
+def test_choose_needs_the_margin_and_breaks_ties_by_cost():
+    cost = {"base": 0, "a": 10, "b": 5, "c": 1}.__getitem__
+    assert tuning.choose({"base": 100.0, "a": 99.0}, "base", cost) == "base"  # 1% < margin
+    assert tuning.choose({"base": 100.0, "a": 95.0}, "base", cost) == "a"
+    # a and b within the tie tolerance: fewer workgroups wins; c is not tied
+    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 90.1, "c": 93.0}, "base", cost) == "b"
+    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 91.0}, "base", cost) == "a"
+
+
+# ---- the plan table of the C ABI (host-only) -----------------------------------------------------
+
+SHAPES = [  # (rows, K, N, group, bits, nproj)
+    (1, 1536, 8960, 64, 4, 2), (1, 8960, 1536, 64, 4, 1), (16, 1536, 8960, 64, 4, 2),
+    (32, 1536, 8960, 64, 4, 1), (1, 5120, 17408, 64, 8, 1), (3, 1024, 1536, 32, 8, 2),
+    (8, 896, 4864, 64, 4, 2), (4, 4864, 896, 64, 4, 1),
+]
+
+
+@pytest.fixture
+def clean_plans():
+    tuning.clear_plans()
+    yield
+    tuning.clear_plans()
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
+    rows, k, n, g, bits, nproj = shape
+    cands = tuning.qmv_plan_candidates(rows, k, n, g, bits, nproj)
+    assert cands and len(set(cands)) == len(cands)
+    import torch
+
+    for dtype in (torch.bfloat16, torch.float16):
+        planner = tuning.qmv_plan(rows, k, n, g, bits, nproj, dtype)
+        if tuning.token_bucket(rows) == rows:
+            assert planner in cands
+    for c in cands:
+        assert c.kernel in ("staged", "register")
+        if c.kernel == "register":
+            assert g != 32 and c.strips == n // 32 and c.tiles == 1
+        else:
+            assert rows <= 16 and n // 32 <= c.strips <= 2 * (n // 32) and c.strips % c.tiles == 0
+        tuning.install_qmv_plan(rows, k, n, g, bits, nproj, torch.bfloat16, c)
+        assert tuning.qmv_plan(rows, k, n, g, bits, nproj, torch.bfloat16) == c
+
+
+def test_installed_plans_are_bucketed_per_dtype_and_size_the_workspace(clean_plans):
+    import torch
+
+    lib = L.lib()
+    k, n = 8960, 1536
+    planner = tuning.qmv_plan(5, k, n, 64, 4, 1, torch.bfloat16)
+    before = lib.mt_affine_qmv_workspace_bytes(5, k, n, 64, 4, 1)
+    wide = max(tuning.qmv_plan_candidates(5, k, n, 64, 4, 1), key=lambda p: p.ksplit)
+    assert wide.ksplit > planner.ksplit
+    tuning.install_qmv_plan(5, k, n, 64, 4, 1, torch.bfloat16, wide)
+    # rows 5..8 share the bucket; 4 and 9 do not; the other dtype keeps the planner's plan
+    for rows in (5, 6, 8):
+        assert tuning.qmv_plan(rows, k, n, 64, 4, 1, torch.bfloat16) == wide
+    assert tuning.qmv_plan(4, k, n, 64, 4, 1, torch.bfloat16) != wide
+    assert tuning.qmv_plan(9, k, n, 64, 4, 1, torch.bfloat16) != wide
+    assert tuning.qmv_plan(5, k, n, 64, 4, 1, torch.float16) == planner
+    # the workspace query covers the installed plan (more K splits, more partial sums)
+    after = lib.mt_affine_qmv_workspace_bytes(5, k, n, 64, 4, 1)
+    assert after == 64 * 1024 + wide.ksplit * 5 * n * 4 > before
+    # a call of 37 rows runs a 32-row and a 5-row dispatch: both are covered
+    assert lib.mt_affine_qmv_workspace_bytes(37, k, n, 64, 4, 1) >= after
+    tuning.install_qmv_plan(5, k, n, 64, 4, 1, torch.bfloat16, None)
+    assert tuning.qmv_plan(5, k, n, 64, 4, 1, torch.bfloat16) == planner
+    assert lib.mt_affine_qmv_workspace_bytes(5, k, n, 64, 4, 1) == before
+
+
+@pytest.mark.parametrize("plan,message", [
+    (QmvPlan("staged", 1, 279, 1), "strips must be in N/32..2N/32"),
+    (QmvPlan("staged", 1, 561, 1), "strips must be in N/32..2N/32"),
+    (QmvPlan("staged", 1, 281, 2), "multiple of tiles"),
+    (QmvPlan("staged", 1, 280, 3), "tiles must be 1 or 2"),
+    (QmvPlan("register", 1, 300, 1), "N/32 strips"),
+    (QmvPlan("register", 1, 280, 2), "N/32 strips"),
+    (QmvPlan("staged", 0, 280, 1), "ksplit must be in 1..K/64"),
+    (QmvPlan("staged", 25, 280, 1), "ksplit must be in 1..K/64"),
+    (QmvPlan("staged", 7, 280, 1), "equal-length splits"),  # 24 steps in 7 splits is 6 of 4
+])
+def test_invalid_qmv_plans_are_rejected(plan, message, clean_plans):
+    import torch
+
+    with pytest.raises(ValueError, match=message):
+        tuning.install_qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16, plan)
+    assert tuning.qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16) != plan
+
+
+def test_plan_rules_that_depend_on_rows_and_groups(clean_plans):
+    import torch
+
+    # the staged kernel takes at most 16 rows; the register kernel no groups of 32
+    with pytest.raises(ValueError, match="more rows than the staged kernel"):
+        tuning.install_qmv_plan(17, 1536, 8960, 64, 4, 1, torch.bfloat16,
+                                QmvPlan("staged", 1, 280, 1))
+    with pytest.raises(ValueError, match="groups of 64 or more"):
+        tuning.install_qmv_plan(1, 1024, 1536, 32, 8, 1, torch.bfloat16,
+                                QmvPlan("register", 1, 48, 1))
+    # one dispatch holds at most 32 rows (16 with groups of 32)
+    with pytest.raises(ValueError, match="rows of one dispatch"):
+        tuning.qmv_plan(33, 1536, 8960, 64, 4, 1, torch.bfloat16)
+    with pytest.raises(ValueError, match="rows of one dispatch"):
+        tuning.qmv_plan(17, 1024, 1536, 32, 8, 1, torch.bfloat16)
+    # every split holds fewer than 64 groups: 140 steps need at least 3 splits
+    with pytest.raises(ValueError, match="too many groups per split"):
+        tuning.install_qmv_plan(1, 8960, 1536, 64, 4, 1, torch.bfloat16,
+                                QmvPlan("register", 2, 48, 1))
+
+
+def test_gemm_plans(clean_plans):
+    import torch
+
+    lib = L.lib()
+    m, k, n = 512, 8960, 1536
+    planner = tuning.gemm_plan(m, k, n, 64, torch.bfloat16)
+    cands = tuning.gemm_plan_candidates(m, k, n, 64)
+    assert planner in cands and {c.tile for c in cands} == {64, 128}
+    before = lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4)
+    pick = next(c for c in cands if c.ksplit == 8 and c.tile == 64)
+    tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, pick)
+    assert tuning.gemm_plan(300, k, n, 64, torch.bfloat16) == pick  # same bucket (512)
+    assert tuning.gemm_plan(m, k, n, 64, torch.float16) == planner
+    assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == 64 * 1024 + 8 * m * n * 4
+    with pytest.raises(ValueError, match="tile must be 64 or 128"):
+        tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, GemmPlan(96, 1))
+    tuning.clear_plans()
+    assert tuning.gemm_plan(m, k, n, 64, torch.bfloat16) == planner
+    assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == before
+
+
+def test_candidate_buffer_contract():
+    lib = L.lib()
+    count = lib.mt_affine_qmv_plan_candidates(1, 1536, 8960, 64, 4, 2, None, 0)
+    assert count > 0
+    buf = (L.QmvPlan * 2)()
+    assert lib.mt_affine_qmv_plan_candidates(1, 1536, 8960, 64, 4, 2, buf, 2) == count
+    assert lib.mt_affine_qmv_plan_candidates(1, 1536, 8960, 64, 4, 2, None, 5) == \
+        L.MT_ERR_INVALID_ARGUMENT
+    assert lib.mt_affine_qmv_plan(1, 1536, 8960, 64, 4, 2, 0, None) == L.MT_ERR_INVALID_ARGUMENT
+    assert lib.mt_affine_qmv_plan_candidates(1, 1500, 8960, 64, 4, 2, None, 0) == \
+        L.MT_ERR_INVALID_ARGUMENT  # K not a multiple of 64
+    assert lib.mt_plans_clear() == L.MT_OK
+
+
+def test_library_reports_the_digest_of_its_sources():
+    digest = L.lib().mt_source_digest().decode()
+    assert len(digest) == 64 and int(digest, 16) >= 0
+    assert digest == build.source_digest(), "the library was built from other sources: rebuild"
