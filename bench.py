@@ -24,7 +24,11 @@ biases, activations in and out. The JSON line also carries:
 * ``ceiling``: the measured streaming-read rate of one launch at the same byte counts;
 * ``cpu_baseline``: the NumPy oracle on this host's cores.
 
-Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]``.
+Every shape first takes its tuned plan (``metile_amd.tuning``, untimed, before the timed
+region; ``tuning`` in the JSON line lists each decision with the planner's and the chosen plan's
+time); ``--no-tune`` keeps the planner's plans.
+
+Usage: ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-tune]``.
 """
 
 from __future__ import annotations
@@ -121,6 +125,17 @@ def copies_for(nbytes):
     return max(2, -(-STACK_BYTES // nbytes))
 
 
+def tune(args, values, weights, bits=BITS):
+    """The plans this shape's dispatches take (untimed, before the timed region): the tuner's
+    decision (``metile_amd.tuning``: every plan the library lists, timed from HIP graphs over
+    cold weights), as the reference's tuned entries and executors do on first use."""
+    if args.no_tune:
+        return
+    from metile_amd import tuning
+
+    tuning.ensure_qmv_plans(values, weights, group_size=GROUP, bits=bits)
+
+
 # ---- sections ---------------------------------------------------------------------------------
 
 
@@ -139,6 +154,9 @@ def section_mlp(mt, gen, device, stream, args):
             return [mt.affine_mlp(x, g, u, d, group_size=GROUP, bits=BITS, residual=res)
                     for (g, u, d) in layers]
 
+        g0, u0, d0 = layers[0]
+        tune(args, x, (*g0, *u0))
+        tune(args, torch.randn(m, INTER, generator=gen, device=device).to(torch.bfloat16), d0)
         steps = args.steps if m == 1 else max(10, args.steps // 4)
         us = timed(stack, stream, steps, args.warmup, LAYERS)
         rows_out[str(m)] = {
@@ -198,6 +216,7 @@ def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
     out = {}
     for m in rows:
         x = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
+        tune(args, x, ws[0], bits)
         us = timed(lambda: [mt.affine_qmv(x, *w, group_size=GROUP, bits=bits) for w in ws],
                    stream, max(10, args.steps // 4), args.warmup, copies)
         total = wb + 2 * m * k + 2 * m * n
@@ -239,6 +258,10 @@ def section_prefill(mt, gen, device, stream, args):
         copies = 4
         ws = [make_affine(gen, device, k, n) for _ in range(copies)]
         x = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
+        if not args.no_tune:
+            from metile_amd import tuning
+
+            tuning.ensure_gemm_plan(x, *ws[0], group_size=GROUP)
         us = timed(lambda: [mt.affine_matmul(x, *w, group_size=GROUP, bits=BITS) for w in ws],
                    stream, max(10, args.steps // 4), args.warmup, copies)
         flops = 2 * 512 * k * n
@@ -372,6 +395,29 @@ def cpu_baseline(budget_s=12.0):
     }
 
 
+def tuning_report(args):
+    """The plan decisions the timed runs took: shape, the planner's plan and the chosen one,
+    each timed by the tuner (us per dispatch)."""
+    if args.no_tune:
+        return {"enabled": False}
+    from metile_amd import tuning
+
+    def short(plan):
+        if plan is None:
+            return "planner"
+        return ",".join(f"{k}={v}" for k, v in plan.items())
+
+    decisions = []
+    for e in tuning.read_json(tuning.cache_path(), {}).values():
+        decisions.append({
+            "op": e.get("op"), "rows": e.get("rows"), "K": e.get("input_features"),
+            "N": e.get("output_features"), "bits": e.get("bits"), "nproj": e.get("nproj", 1),
+            "planner": short(e.get("planner")), "chosen": short(e.get("plan")),
+            "planner_us": e.get("planner_us"), "chosen_us": e.get("chosen_us")})
+    decisions.sort(key=lambda d: (d["op"], d["nproj"], d["K"], d["N"], d["rows"]))
+    return {"enabled": True, "switch_margin": tuning.SWITCH_MARGIN, "decisions": decisions}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -386,7 +432,14 @@ def main():
                     help="only the eager launches profiled by the HBM-traffic counter runs")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only eager config-4 GEMM launches, for instruction-counter runs")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="run every shape on the planner's plan (no plan tuning)")
     args = ap.parse_args()
+    if not args.no_tune and "METILE_AMD_CACHE_DIR" not in os.environ:
+        # decisions are measured in this run (and reported), not read from an earlier one
+        import tempfile
+
+        os.environ["METILE_AMD_CACHE_DIR"] = tempfile.mkdtemp(prefix="metile_amd_bench_")
     if args.gpus != 1:
         print("bench.py measures one GPU only: the hot path runs on a single MI355X and this "
               "build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -454,6 +507,7 @@ def main():
             "down_achieved": round(kernel["down_bytes"] / kernel["down_us"] / 1e3, 1),
         },
         "native_layout": kernel["native_layout"],
+        "tuning": tuning_report(args),
     }
     if configs:
         result["configs"] = configs
