@@ -10,7 +10,13 @@ compositions for checking kernels against its semantics.
 from ._lib import MetileError, version
 from .dense import DenseWeight, dense_qmv, dense_swiglu, mlx_dense_residual_qmv, mlx_dense_swiglu
 from .fidelity import accuracy_compatible, affine_swiglu_compatible
-from .model import QuantizedLinear, patch_quantized_mlp, quantize_mlp, restore_patches
+from .model import (
+    QuantizedLinear,
+    patch_graph_fusion,
+    patch_quantized_mlp,
+    quantize_mlp,
+    restore_patches,
+)
 from .native import native_affine_matmul, native_affine_residual_qmv, native_affine_swiglu
 from .quantize import CompressedDownWeight, affine_quantize
 from .quantized import (
@@ -38,6 +44,7 @@ __all__ = [
     "CompressedDownWeight",
     "QuantizedLinear",
     "affine_quantize",
+    "patch_graph_fusion",
     "patch_quantized_mlp",
     "quantize_mlp",
     "restore_patches",

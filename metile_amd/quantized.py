@@ -500,8 +500,6 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
     the native compositions (the reference tuner's fidelity gate), and returns
     ``execute(values, residual) = down(swiglu(values)) + residual`` over the repacked weights
     (one C-ABI call)."""
-    from .native import native_affine_residual_qmv, native_affine_swiglu
-
     # Every argument check first (on a shape-only stand-in for the hidden activation), then
     # the kernels.
     _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
@@ -513,6 +511,23 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
     gate = (affine_repack(gate_weight, bits=bits), gate_scales, gate_biases)
     up = (affine_repack(up_weight, bits=bits), up_scales, up_biases)
     down = (affine_repack(down_weight, bits=bits), down_scales, down_biases)
+    mlx = ((gate_weight, gate_scales, gate_biases), (up_weight, up_scales, up_biases),
+           (down_weight, down_scales, down_biases))
+    return bind_mlp_executor(sample_values, mlx, (gate, up, down), sample_residual,
+                             group_size=group_size, bits=bits, autotune=autotune)
+
+
+def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size=64, bits=4,
+                      autotune=True):
+    """The steps of ``mlx_affine_mlp_executor`` after its argument checks, for weights already
+    repacked: ``mlx`` and ``packed`` are the (gate, up, down) triples in MLX layout (for the
+    native compositions the gates compare against) and repacked (for the kernels). Tunes both
+    stages at the sample's shape, gates them, returns ``execute(values, residual)``."""
+    from .native import native_affine_residual_qmv, native_affine_swiglu
+
+    gate, up, down = packed
+    (gate_weight, gate_scales, gate_biases), (up_weight, up_scales, up_biases), \
+        (down_weight, down_scales, down_biases) = mlx
     if autotune:
         _tuning.ensure_qmv_plans(sample_values, (*gate, *up), group_size=group_size, bits=bits)
     hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)

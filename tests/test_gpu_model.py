@@ -6,8 +6,10 @@
 * Token equality, after the reference's ``tests/test_model_equivalence.py``: tiny Qwen2 and
   Llama models (random weights from a seeded config; no checkpoints are available offline)
   have their MLP projections quantized, then decode greedily once with the original gated-MLP
-  forward (three projections, the activation in torch) and once patched to the fused SwiGLU
-  kernel. The two differ only in where SwiGLU rounds, so the logits agree to a few bf16 units
+  forward (three projections, the activation in torch) and once patched: to the fused SwiGLU
+  kernel (``patch_quantized_mlp``), or to one MLP executor call per layer with the residual
+  add in the down projection (``patch_graph_fusion``); unquantized bf16 models patched by
+  ``patch_graph_fusion`` run the dense SwiGLU and residual kernels at one row. The two differ only in where SwiGLU rounds, so the logits agree to a few bf16 units
   in the last place and the tokens must agree; a divergence is allowed only at a step where
   the measured logit difference is large enough to reorder the two tokens involved.
   Attention runs in float32 (bf16 batched products with transposed operands are kept off the
@@ -82,7 +84,7 @@ def _fp32_attention(module, query, key, value, attention_mask, **kwargs):
     return out.to(query.dtype), weights
 
 
-def _tiny_model(family):
+def _tiny_model(family, quantize=True):
     transformers = pytest.importorskip("transformers")
     transformers.AttentionInterface.register("metile_fp32_sdpa", _fp32_attention)
     common = dict(hidden_size=256, intermediate_size=768, num_hidden_layers=3,
@@ -97,7 +99,8 @@ def _tiny_model(family):
         model = transformers.LlamaForCausalLM(cfg)
     model.config._attn_implementation = "metile_fp32_sdpa"
     model = model.to(device="cuda", dtype=torch.bfloat16).eval()
-    assert mt.quantize_mlp(model) == 3
+    if quantize:
+        assert mt.quantize_mlp(model) == 3
     return model
 
 
@@ -115,27 +118,31 @@ def _greedy(model, prompt, steps):
     return tokens, logits
 
 
-@pytest.mark.parametrize("family", ["qwen2", "llama"])
-def test_patched_mlp_decodes_the_same_tokens(family):
-    model = _tiny_model(family)
+def _decode_patched(model, patch, counted, steps=24):
+    """Greedy decode unpatched, then with ``patch(model)`` applied while the module-level
+    function ``counted`` of ``metile_amd.model`` counts its calls (with a residual or not)."""
     prompt = torch.randint(0, 1024, (1, 12), generator=torch.Generator().manual_seed(7)).cuda()
-    base_tokens, base_logits = _greedy(model, prompt, 24)
-    calls = {"fused": 0}
-    original = mt.model._execute_quantized_mlp
+    base = _greedy(model, prompt, steps)
+    calls = {"plain": 0, "residual": 0}
+    original = getattr(mt.model, counted)
 
-    def counting(module, values):
-        calls["fused"] += 1
-        return original(module, values)
+    def counting(module, values, *rest):
+        calls["residual" if rest and rest[0] is not None else "plain"] += 1
+        return original(module, values, *rest)
 
-    mt.model._execute_quantized_mlp = counting
-    replacements = mt.patch_quantized_mlp(model)
+    setattr(mt.model, counted, counting)
+    replacements = patch(model)
     try:
-        tokens, logits = _greedy(model, prompt, 24)
+        patched = _greedy(model, prompt, steps)
     finally:
         mt.restore_patches(replacements)
-        mt.model._execute_quantized_mlp = original
-    assert calls["fused"] == 3 * 25  # every layer, prompt and 24 decode steps
+        setattr(mt.model, counted, original)
     assert len(replacements) == 1
+    return base, patched, calls
+
+
+def _assert_same_decode(family, base, patched):
+    (base_tokens, base_logits), (tokens, logits) = base, patched
     scale = max(float(l.abs().max()) for l in base_logits)
     worst = 0.0
     for step, (a, b) in enumerate(zip(base_tokens, tokens)):
@@ -150,6 +157,32 @@ def test_patched_mlp_decodes_the_same_tokens(family):
             break
     print(f"[{family}] tokens equal: {base_tokens == tokens}, worst logit difference "
           f"{worst:.4f} of the logit scale", flush=True)
+
+
+@pytest.mark.parametrize("family", ["qwen2", "llama"])
+def test_patched_mlp_decodes_the_same_tokens(family):
+    model = _tiny_model(family)
+    base, patched, calls = _decode_patched(model, mt.patch_quantized_mlp, "_execute_quantized_mlp")
+    assert calls == {"plain": 3 * 25, "residual": 0}  # every layer, prompt and 24 steps
+    _assert_same_decode(family, base, patched)
+
+
+@pytest.mark.parametrize("family", ["qwen2", "llama"])
+def test_graph_fusion_runs_the_mlp_executor_with_the_residual(family):
+    model = _tiny_model(family)
+    base, patched, calls = _decode_patched(model, mt.patch_graph_fusion, "_execute_quantized_mlp")
+    # every layer of the prompt and of each step: one executor call, residual fused
+    assert calls == {"plain": 0, "residual": 3 * 25}
+    assert len(mt.model._quantized_mlp_executor_cache) >= 3
+    _assert_same_decode(family, base, patched)
+
+
+@pytest.mark.parametrize("family", ["qwen2", "llama"])
+def test_graph_fusion_runs_dense_mlps_at_one_row(family):
+    model = _tiny_model(family, quantize=False)
+    base, patched, calls = _decode_patched(model, mt.patch_graph_fusion, "_execute_dense_mlp")
+    assert calls == {"plain": 0, "residual": 3 * 24}  # decode steps only (one row each)
+    _assert_same_decode(family, base, patched)
 
 
 def test_prefill_rows_take_the_gemm_and_match_the_decode_path():

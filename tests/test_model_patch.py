@@ -71,3 +71,36 @@ def test_quantizer_guards():
         mt.CompressedDownWeight.quantize(w[0])
     with pytest.raises(ValueError, match="must be affine8 or mxfp8"):
         mt.CompressedDownWeight.quantize(w, format="int3")
+
+
+def test_graph_fusion_patches_recognised_blocks_and_falls_back_off_device():
+    model = _tiny()
+    block_class = type(model.model.layers[0])
+    original = block_class.forward
+    ids = torch.arange(10).view(1, 10)
+    with torch.no_grad():
+        want = model(ids).logits
+        reps = mt.patch_graph_fusion(model)
+        try:
+            assert len(reps) == 1 and block_class.forward is not original
+            assert block_class.forward._metile_original is original
+            assert mt.patch_graph_fusion(model) == []  # already patched
+            got = model(ids).logits  # host tensors: every block takes the original forward
+        finally:
+            mt.restore_patches(reps)
+    assert block_class.forward is original
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+
+
+def test_graph_fusion_leaves_unrecognised_blocks_alone():
+    model = _tiny()
+    layer_class = type(model.model.layers[0])
+
+    class CustomLayer(layer_class):  # same structure, not a registered class
+        pass
+
+    for layer in model.model.layers:
+        layer.__class__ = CustomLayer
+    assert mt.patch_graph_fusion(model) == []
+    with pytest.raises(ValueError, match="minimum rows must be positive"):
+        mt.patch_graph_fusion(model, quantized_mlp_min_rows=0)
