@@ -137,9 +137,9 @@ int mt_affine_mlp_repacked(const void* x, const uint32_t* gate_packed, const voi
 /* Workspace bytes mt_affine_gemm needs (0 when K is not split). */
 size_t mt_affine_gemm_workspace_bytes(int M, int K, int N, int group_size, int bits);
 
-/* y = x @ dequantize(w_q)^T for many rows (prefill): the codes are dequantized to the
- * activation type (q*s + b in fp32, then rounded) in LDS and multiplied on the matrix cores
- * with fp32 accumulation. Replaces mlx_affine_matmul / lower_affine_matmul
+/* y = x @ dequantize(w_q)^T for many rows (prefill) on the matrix cores with fp32 accumulation.
+ * Dequantization stays exact: the codes enter the MFMAs as exact 16-bit floats (offset + q) and
+ * each 64-wide step's partial gets its group's scale and bias terms in fp32. Replaces mlx_affine_matmul / lower_affine_matmul
  * (metile/backends/mlx_affine.py:359-406, metile/compiler/affine_quantized.py:7-99).
  * bits = 4; group_size a power of two >= 64 dividing K; K % 64 == 0; N % 32 == 0. */
 int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const void* biases,

@@ -2,16 +2,17 @@
 // many rows (reference: lower_affine_matmul, metile/compiler/affine_quantized.py:7-99, and its
 // dispatcher mlx_affine_matmul, metile/backends/mlx_affine.py:359-406).
 //
-// Design: a workgroup computes a BM x BN output tile with a 2 x 2 grid of waves, each wave
-// TM x TN tiles of MFMA 32x32x16 (fp32 accumulate). The K loop runs in 64-wide steps through a
-// double-buffered LDS pipeline: the next step's activation tile and packed codes are loaded
-// into registers while the current step's MFMAs run from LDS, then the codes are turned into
-// exact 16-bit floats (offset + q) and written to the other LDS buffer with the activation
-// tile, the per-row sums of the activation tile and the per-column scale and bias.
+// Design: a workgroup of WM x WN waves computes a (32 TM WM) x (32 TN WN) output tile; each
+// wave owns TM x TN tiles of MFMA 32x32x16 (fp32 accumulate). The K loop runs in 64-wide steps
+// through a double-buffered LDS pipeline with one barrier per step: the next step's activation
+// tile and packed codes are loaded into registers while the current step's MFMAs run from LDS,
+// then stored to the other buffer: the codes as exact 16-bit floats (offset + q), the
+// activations as loaded, and each column's scale.
 // Dequantization stays exact: each step's MFMA partial t = sum_k x_k (offset + q_k) gets its
-// group's affine terms in fp32, acc += s * t + (b - offset * s) * sum_k x_k, exactly as in the
-// small-row kernel. Rows beyond M and columns beyond N read zero through the buffer range
-// check and are not stored.
+// group's affine terms in fp32, acc += s * t + (b - offset * s) * X with X = sum_k x_k, as in
+// the small-row kernel. X is summed while staging: eight lanes hold a row's eight 16-byte
+// chunks (dot products with ones) and combine with DPP moves. Rows beyond M and columns beyond
+// N read zero through the buffer range check and are not stored.
 #include "common.h"
 #include "affine_gemm.h"
 
@@ -23,13 +24,34 @@ constexpr int kBK = 64;        // K per pipeline step
 constexpr int kPad = 8;        // LDS row padding, in 16-bit elements
 constexpr int kLdsRow = kBK + kPad;
 
-template <int DT, int TM, int TN>
-__global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p) {
-  constexpr int BM = 64 * TM;
-  constexpr int BN = 64 * TN;
-  constexpr int kAChunks = BM * kBK * 2 / 16 / 256;  // 16-byte activation chunks per thread
+// c + a.lo + a.hi: a pair of 16-bit floats summed into fp32 (a dot product with ones). The word
+// arrives as a scalar argument: with this compiler, __builtin_bit_cast applied directly to an
+// element of a vector value read the vector's first word instead.
+template <int DT>
+__device__ __forceinline__ float pair_sum(uint32_t a, float c) {
+  if constexpr (DT == kBF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a),
+                                  __builtin_bit_cast(f16x2, 0x3c003c00u), c, false);
+}
+
+// Sum of the eight 16-bit values of a 16-byte chunk, fp32 accumulate.
+template <int DT>
+__device__ __forceinline__ float chunk_sum(u32x4 v) {
+  return pair_sum<DT>(v.w, pair_sum<DT>(v.z, pair_sum<DT>(v.y, pair_sum<DT>(v.x, 0.0f))));
+}
+
+template <int DT, int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const GemmParams p) {
+  constexpr int kThreads = 64 * WM * WN;
+  constexpr int BM = 32 * TM * WM;
+  constexpr int BN = 32 * TN * WN;
+  constexpr int kAChunks = BM * kBK * 2 / 16 / kThreads;  // 16-byte activation chunks/thread
   constexpr float kOff = CodeOffset<4, DT>::value;
-  static_assert(kAChunks >= 1, "tile too small");
+  static_assert(kAChunks >= 1 && BM * kBK * 2 / 16 % kThreads == 0, "tile too small");
+  static_assert(2 * BN <= kThreads, "one thread per half column of codes");
 
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][kLdsRow];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][kLdsRow];
@@ -39,7 +61,7 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int j = lane & 31, h = lane >> 5;
   const int M = p.M, K = p.K, N = p.N;
   const int m0 = blockIdx.y * BM;
@@ -55,12 +77,13 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s, (uint32_t)N * groups_per_row * 2u);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b, (uint32_t)N * groups_per_row * 2u);
 
-  // Activation tile: chunk c = tid + 256 i covers row c / 8, 16 bytes (c % 8) of the step.
+  // Activation tile: chunk c = tid + kThreads i covers row c / 8, 16 bytes (c % 8) of the step;
+  // the eight chunks of a row sit in eight consecutive lanes (kThreads is a multiple of 8).
   uint32_t a_off[kAChunks];
   int a_row[kAChunks], a_col[kAChunks];
 #pragma unroll
   for (int i = 0; i < kAChunks; ++i) {
-    const int c = tid + 256 * i;
+    const int c = tid + kThreads * i;
     a_row[i] = c >> 3;
     a_col[i] = (c & 7) * 8;
     const int gr = m0 + a_row[i];
@@ -73,9 +96,6 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   const bool col_ok = b_active && gcol < N;
   const uint32_t b_off = col_ok ? (uint32_t)gcol * row_bytes + 16u * b_half : kOOB;
   const uint32_t g_off = col_ok ? (uint32_t)gcol * groups_per_row * 2u : kOOB;
-  // Row sums: thread t < 2*BM sums half (t & 1) of row t >> 1 of the activation tile.
-  const bool x_active = tid < 2 * BM;
-  const int x_row = tid >> 1, x_half = tid & 1;
 
   u32x4 ra[kAChunks];
   u32x4 rc;
@@ -91,8 +111,12 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   };
   auto store_step = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < kAChunks; ++i)
+    for (int i = 0; i < kAChunks; ++i) {
       *reinterpret_cast<u32x4*>(&As[buf][a_row[i]][a_col[i]]) = ra[i];
+      // Row sum of the step: this lane's eight elements, then the row's eight lanes.
+      const float sum = group_sum8(chunk_sum<DT>(ra[i]));
+      if ((tid & 7) == 0) Xs[buf][a_row[i]] = sum;
+    }
     if (b_active) {
 #pragma unroll
       for (int q = 0; q < 4; ++q)
@@ -103,17 +127,6 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
         Bp[buf][b_col] = __builtin_fmaf(-kOff, sf, act_to_f32<DT>(rbv));
       }
     }
-  };
-  // Per-row sums of a stored activation tile (call after the barrier that publishes it).
-  auto sum_rows = [&](int buf) {
-    float acc = 0.0f;
-    if (x_active) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        acc = sum8<DT>(*reinterpret_cast<const u32x4*>(&As[buf][x_row][32 * x_half + 8 * q]), acc);
-    }
-    acc += dpp_read<kDppXor1>(acc);
-    if (x_active && x_half == 0) Xs[buf][x_row] = acc;
   };
 
   f32x16 acc[TM][TN];
@@ -126,8 +139,6 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
     load_step(s_beg);
     store_step(0);
   }
-  __syncthreads();
-  if (s_beg < s_end) sum_rows(0);
   __syncthreads();
   const f32x16 zero16 = (f32x16){0};
   for (int st = s_beg; st < s_end; ++st) {
@@ -173,9 +184,8 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
         }
       }
     }
+    // The other buffer was last read in the previous step, before that step's barrier.
     if (more) store_step(buf ^ 1);
-    __syncthreads();
-    if (more) sum_rows(buf ^ 1);
     __syncthreads();
   }
 
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
   }
   __syncthreads();
   if (!last_flag) return;
-  for (int o = tid; o < BM * BN; o += 256) {
+  for (int o = tid; o < BM * BN; o += kThreads) {
     const int row = m0 + o / BN, col = n0 + o % BN;
     if (row >= M || col >= N) continue;
     const float v = sum_partials(p.partial + (size_t)row * N + col, (size_t)M * N, p.ksplit);
@@ -221,17 +231,19 @@ __global__ __launch_bounds__(256, 2) void affine_gemm_kernel(const GemmParams p)
     __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int TM, int TN>
+template <int DT, int WM, int WN, int TM, int TN>
 hipError_t launch_tile(const GemmParams& p, hipStream_t stream) {
-  const dim3 grid((p.N + 64 * TN - 1) / (64 * TN), (p.M + 64 * TM - 1) / (64 * TM), p.ksplit);
-  affine_gemm_kernel<DT, TM, TN><<<grid, 256, 0, stream>>>(p);
+  constexpr int BM = 32 * TM * WM, BN = 32 * TN * WN;
+  const dim3 grid((p.N + BN - 1) / BN, (p.M + BM - 1) / BM, p.ksplit);
+  affine_gemm_kernel<DT, WM, WN, TM, TN><<<grid, 64 * WM * WN, 0, stream>>>(p);
   return hipGetLastError();
 }
 
+// 128 x 128 tiles: four waves of 64 x 64; 64 x 64 tiles: four waves of 32 x 32.
 template <int DT>
 hipError_t launch_dt(const GemmParams& p, hipStream_t stream) {
-  if (p.tile == 2) return launch_tile<DT, 2, 2>(p, stream);
-  return launch_tile<DT, 1, 1>(p, stream);
+  if (p.tile == 2) return launch_tile<DT, 2, 2, 2, 2>(p, stream);
+  return launch_tile<DT, 2, 2, 1, 1>(p, stream);
 }
 
 }  // namespace
