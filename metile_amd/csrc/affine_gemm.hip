@@ -24,25 +24,6 @@ constexpr int kBK = 64;        // K per pipeline step
 constexpr int kPad = 8;        // LDS row padding, in 16-bit elements
 constexpr int kLdsRow = kBK + kPad;
 
-// c + a.lo + a.hi: a pair of 16-bit floats summed into fp32 (a dot product with ones). The word
-// arrives as a scalar argument: with this compiler, __builtin_bit_cast applied directly to an
-// element of a vector value read the vector's first word instead.
-template <int DT>
-__device__ __forceinline__ float pair_sum(uint32_t a, float c) {
-  if constexpr (DT == kBF16)
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
-                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), c, false);
-  else
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a),
-                                  __builtin_bit_cast(f16x2, 0x3c003c00u), c, false);
-}
-
-// Sum of the eight 16-bit values of a 16-byte chunk, fp32 accumulate.
-template <int DT>
-__device__ __forceinline__ float chunk_sum(u32x4 v) {
-  return pair_sum<DT>(v.w, pair_sum<DT>(v.z, pair_sum<DT>(v.y, pair_sum<DT>(v.x, 0.0f))));
-}
-
 template <int DT, int WM, int WN, int TM, int TN>
 __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const GemmParams p) {
   constexpr int kThreads = 64 * WM * WN;
@@ -114,7 +95,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const Gemm
     for (int i = 0; i < kAChunks; ++i) {
       *reinterpret_cast<u32x4*>(&As[buf][a_row[i]][a_col[i]]) = ra[i];
       // Row sum of the step: this lane's eight elements, then the row's eight lanes.
-      const float sum = group_sum8(chunk_sum<DT>(ra[i]));
+      const float sum = group_sum8(sum8<DT>(ra[i], 0.0f));
       if ((tid & 7) == 0) Xs[buf][a_row[i]] = sum;
     }
     if (b_active) {

@@ -208,20 +208,24 @@ __device__ __forceinline__ float hi16(uint32_t w) {
   else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-// Sum of the 8 16-bit floats held in a u32x4, added to acc in element order in fp32.
-// (Plain adds: a probe of v_dot2_f32_bf16 against ones returned wrong sums for negative
-// inputs, so the dot instructions are not used for this.)
+// acc + a.lo + a.hi for a word holding two 16-bit floats: one dot product with (1, 1), fp32
+// accumulate. The word must arrive as a scalar: with this compiler, __builtin_bit_cast applied
+// directly to an element of a vector value read the vector's first word instead (which is what
+// made dot products fed that way return wrong sums).
+template <int DT>
+__device__ __forceinline__ float pair_sum(uint32_t a, float acc) {
+  if constexpr (DT == kBF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a),
+                                  __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+}
+
+// Sum of the 8 16-bit floats held in a u32x4, added to acc in fp32, two per instruction.
 template <int DT>
 __device__ __forceinline__ float sum8(u32x4 v, float acc) {
-  acc += lo16<DT>(v.x);
-  acc += hi16<DT>(v.x);
-  acc += lo16<DT>(v.y);
-  acc += hi16<DT>(v.y);
-  acc += lo16<DT>(v.z);
-  acc += hi16<DT>(v.z);
-  acc += lo16<DT>(v.w);
-  acc += hi16<DT>(v.w);
-  return acc;
+  return pair_sum<DT>(v.w, pair_sum<DT>(v.z, pair_sum<DT>(v.y, pair_sum<DT>(v.x, acc))));
 }
 
 // ---- lane exchanges within a row of 16 lanes (DPP: one VALU instruction, no LDS trip) ----
