@@ -80,10 +80,21 @@ def repacked(mt, triple, bits=BITS):
     return mt.affine_repack(w, bits=bits), s, b
 
 
+# Untimed replays continue for at least this long before timing starts: the first replays after
+# an idle host phase (allocation, capture, tuning) ran up to 18% slower (prefill down GEMM:
+# 57.2 us on the first graph of a shape, 48.7 us once clocks had settled).
+MIN_WARM_MS = 25.0
+
+
 def time_graph(graph, stream, steps, warmup):
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < MIN_WARM_MS:
+        for _ in range(max(warmup, 1)):
+            graph.replay()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record(stream)
@@ -255,7 +266,7 @@ def section_prefill(mt, gen, device, stream, args):
     """INT4 prefill GEMM at M=512, Qwen2.5-1.5B up and down shapes (config 4)."""
     out = {}
     for name, k, n in (("up", HIDDEN, INTER), ("down", INTER, HIDDEN)):
-        copies = 4
+        copies = copies_for(proj_weight_bytes(k, n))
         ws = [make_affine(gen, device, k, n) for _ in range(copies)]
         x = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
         if not args.no_tune:
@@ -265,7 +276,7 @@ def section_prefill(mt, gen, device, stream, args):
         us = timed(lambda: [mt.affine_matmul(x, *w, group_size=GROUP, bits=BITS) for w in ws],
                    stream, max(10, args.steps // 4), args.warmup, copies)
         flops = 2 * 512 * k * n
-        out[name] = {"K": k, "N": n, "M": 512, "us": round(us, 3),
+        out[name] = {"K": k, "N": n, "M": 512, "copies": copies, "us": round(us, 3),
                      "TFLOPs": round(flops / us / 1e6, 1),
                      "frac_of_mfma_peak": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
         del ws
