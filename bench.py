@@ -7,11 +7,13 @@ from HBM. A step is one pass of the hot path over one batch: the M=1 decode row 
 layer MLPs (fused gate/up SwiGLU kernel, then the down projection with the residual epilogue),
 replayed from a HIP graph whose outputs are first checked bit-for-bit against an eager run.
 Weights are seeded synthetic data of the BASELINE recipe (codes uniform in 0..15,
-scale = |N(0,1)|*0.02 in bf16, bias = -8*scale), generated in MLX's layout and repacked once,
-ahead of time and outside every timed region, to the step-major layout the small-row kernels
-read fastest (``affine_repack``; the reference's executors likewise run their fastest schedules
-on weights repacked ahead of time). The results are bit-identical to those over MLX's layout,
-which is also timed at M=1 (``native_layout``).
+scale = |N(0,1)|*0.02 in bf16, bias = -8*scale), generated in MLX's layout. Each stage's
+weights are kept in the code layout its tuned M=1 plan reads fastest, decided with the plans
+ahead of time and outside every timed region (``metile_amd.tuning.ensure_qmv_layout``, as the
+library's executors do when they bind; ``layouts`` in the JSON line): the step-major repack of
+``affine_repack`` or MLX's rows (the reference's executors likewise choose between their
+repacked and plain schedules). The results are bit-identical in either layout; all-MLX codes are
+also timed at M=1 (``native_layout``).
 
 ``value`` is the whole-job algorithmic HBM throughput of the M=1 step: packed weights, scales,
 biases, activations in and out. The JSON line also carries:
@@ -147,15 +149,39 @@ def tune(args, values, weights, bits=BITS):
     tuning.ensure_qmv_plans(values, weights, group_size=GROUP, bits=bits)
 
 
+def choose_layout(args, values, native, packed, bits=BITS):
+    """The code layout one projection's weights are kept in (untimed, before the timed region):
+    the tuner times every plan over both layouts (``metile_amd.tuning.ensure_qmv_layout``) and
+    keeps the faster pair, as the library's executors do when they bind; ``--no-tune`` keeps
+    the repacked codes. ``native``/``packed``: the weights as for ``tune``, in MLX's layout and
+    repacked."""
+    if args.no_tune:
+        return "repacked"
+    from metile_amd import tuning
+
+    return tuning.ensure_qmv_layout(values, {"repacked": packed, "mlx": native},
+                                    group_size=GROUP, bits=bits)
+
+
 # ---- sections ---------------------------------------------------------------------------------
 
 
 def section_mlp(mt, gen, device, stream, args):
     native = [make_layer(gen, device) for _ in range(LAYERS)]
-    layers = [tuple(repacked(mt, t) for t in layer) for layer in native]
+    packed = [tuple(repacked(mt, t) for t in layer) for layer in native]
     torch.cuda.synchronize()
+    # each stage's weights stay in the layout its M=1 plan reads fastest, for every row count
+    (ng, nu, nd), (pg, pu, pd) = native[0], packed[0]
+    x1 = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    h1 = torch.randn(1, INTER, generator=gen, device=device).to(torch.bfloat16)
+    up_layout = choose_layout(args, x1, (*ng, *nu), (*pg, *pu))
+    down_layout = choose_layout(args, h1, nd, pd)
+    layers = [((p if up_layout == "repacked" else n)[0], (p if up_layout == "repacked" else n)[1],
+               (p if down_layout == "repacked" else n)[2]) for n, p in zip(native, packed)]
+    del packed
+    kernel = {"layouts": {"gate_up": up_layout, "down": down_layout}}
     wbytes = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
-    rows_out, kernel, step_ms = {}, {}, None
+    rows_out, step_ms = {}, None
     rows = sorted({1, *(int(v) for v in args.rows.split(","))})
     for m in rows:
         x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
@@ -220,10 +246,15 @@ def section_mlp(mt, gen, device, stream, args):
 
 
 def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
-    """One affine projection over a rotation of distinct copies (configs 0 and 3)."""
+    """One affine projection over a rotation of distinct copies (configs 0 and 3), its codes
+    in the layout the tuner picks at the first row count."""
     wb = proj_weight_bytes(k, n, bits)
     copies = copies_for(wb)
-    ws = [repacked(mt, make_affine(gen, device, k, n, bits), bits) for _ in range(copies)]
+    ws = [make_affine(gen, device, k, n, bits) for _ in range(copies)]
+    x = torch.randn(rows[0], k, generator=gen, device=device).to(torch.bfloat16)
+    layout = choose_layout(args, x, ws[0], repacked(mt, ws[0], bits), bits)
+    if layout == "repacked":
+        ws = [repacked(mt, w, bits) for w in ws]
     out = {}
     for m in rows:
         x = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
@@ -235,7 +266,7 @@ def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
                        "frac_of_peak": round(total / us / 1e3 / HBM_PEAK_GBS, 4)}
     del ws
     return {"K": k, "N": n, "bits": bits, "group_size": GROUP, "copies": copies,
-            "bytes_per_call_M1": wb + 2 * k + 2 * n, "rows": out}
+            "layout": layout, "bytes_per_call_M1": wb + 2 * k + 2 * n, "rows": out}
 
 
 def section_dense(mt, gen, device, stream, args):
@@ -424,7 +455,8 @@ def tuning_report(args):
             "op": e.get("op"), "rows": e.get("rows"), "K": e.get("input_features"),
             "N": e.get("output_features"), "bits": e.get("bits"), "nproj": e.get("nproj", 1),
             "planner": short(e.get("planner")), "chosen": short(e.get("plan")),
-            "planner_us": e.get("planner_us"), "chosen_us": e.get("chosen_us")})
+            "planner_us": e.get("planner_us"), "chosen_us": e.get("chosen_us"),
+            **({"layout": e["layout"]} if "layout" in e else {})})
     decisions.sort(key=lambda d: (d["op"], d["nproj"], d["K"], d["N"], d["rows"]))
     return {"enabled": True, "switch_margin": tuning.SWITCH_MARGIN, "decisions": decisions}
 
@@ -499,7 +531,9 @@ def main():
         "config": {
             "workload": "INT4 fused SwiGLU MLP, Qwen2.5-1.5B shape (H=1536, I=8960, g64), "
                         "M=1 decode row through 28 distinct layers per step (config 1); codes "
-                        "repacked step-major once, ahead of time",
+                        f"kept in the layout the tuner picked per stage (gate/up "
+                        f"{kernel['layouts']['gate_up']}, down {kernel['layouts']['down']}), "
+                        "prepared once, ahead of time",
             "layers": LAYERS, "hidden": HIDDEN, "intermediate": INTER, "group_size": GROUP,
             "bits": BITS, "rows": 1,
         },
@@ -517,6 +551,7 @@ def main():
             "down_avg_kernel_us": round(kernel["down_us"], 3),
             "down_achieved": round(kernel["down_bytes"] / kernel["down_us"] / 1e3, 1),
         },
+        "layouts": kernel["layouts"],
         "native_layout": kernel["native_layout"],
         "tuning": tuning_report(args),
     }

@@ -132,6 +132,23 @@ int mt_affine_mlp_repacked(const void* x, const uint32_t* gate_packed, const voi
                            int I, int group_size, int bits, int dtype, void* workspace,
                            size_t workspace_bytes, void* stream);
 
+/* Code layouts of one weight: MLX's rows or the step-major repack of mt_affine_repack. */
+typedef enum mt_code_layout { MT_LAYOUT_MLX = 0, MT_LAYOUT_REPACKED = 1 } mt_code_layout;
+
+/* mt_affine_mlp with the gate and up codes in `up_layout` and the down codes in `down_layout`,
+ * so that each weight can be kept in the layout its plan reads fastest (at one row of
+ * Qwen2.5-1.5B's MLP: gate/up repacked for the staged kernel, down in MLX rows for the GEMV
+ * kernel). Same arguments, workspace and results as mt_affine_mlp, bit for bit. The reference's
+ * executors likewise pick per stage between their repacked and plain schedules
+ * (metile/backends/mlx_quantized.py:949-967,1082-1100). */
+int mt_affine_mlp_layouts(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                          const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                          const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                          const void* down_biases, const void* residual, void* y, int M, int H,
+                          int I, int group_size, int bits, int dtype, int up_layout,
+                          int down_layout, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* ---- prefill (many rows) ---------------------------------------------------------------- */
 
 /* Workspace bytes mt_affine_gemm needs (0 when K is not split). */
@@ -173,8 +190,14 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
 
 /* How one small-row dispatch runs: the kernel, the number of K splits, the number of column
  * strips (workgroup columns; N/32 for the register kernel, N/32 to 2N/32 for the staged kernel)
- * and the strips per workgroup (1 or 2, staged kernel only). */
-typedef enum mt_qmv_kernel { MT_QMV_STAGED = 1, MT_QMV_REGISTER = 2 } mt_qmv_kernel;
+ * and the strips per workgroup (1 or 2, staged kernel only). The GEMV kernel (up to 4 rows)
+ * never splits K: its strips are N/4 or N/2 (4 or 2 columns per workgroup) and `tiles` holds
+ * its waves per workgroup (2, 4 or 8). */
+typedef enum mt_qmv_kernel {
+  MT_QMV_STAGED = 1,
+  MT_QMV_REGISTER = 2,
+  MT_QMV_GEMV = 3
+} mt_qmv_kernel;
 typedef struct mt_qmv_plan {
   int kernel;
   int ksplit;

@@ -22,6 +22,9 @@ MT_F16 = 1
 
 MT_QMV_STAGED = 1
 MT_QMV_REGISTER = 2
+MT_QMV_GEMV = 3
+MT_LAYOUT_MLX = 0
+MT_LAYOUT_REPACKED = 1
 
 
 class QmvPlan(ctypes.Structure):
@@ -62,6 +65,8 @@ SIGNATURES = {
                                        _P, _Z, _P]),
     "mt_affine_mlp_repacked": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                     _I, _I, _I, _P, _Z, _P]),
+    "mt_affine_mlp_layouts": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                   _I, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_affine_gemm_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "mt_affine_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_stream_read": (_I, [_P, _Z, _P, _I, _P]),

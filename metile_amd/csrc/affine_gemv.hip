@@ -1,0 +1,227 @@
+// Small-row affine QMV / SwiGLU without a split-K hand-off (gfx950), for projections whose K
+// is long and N short (the down projection: K = 8960, N = 1536): the same semantics as the
+// staged kernel (kernels/affine_qmv.py:57-214; mlx_affine_qmv, mlx_affine_swiglu,
+// metile/backends/mlx_quantized.py:691-751,1645-1720).
+//
+// A workgroup owns COLS output columns (2 or 4) and all of K, so no partial sum leaves it. Its
+// lanes (1 to 8 waves; the plan picks the fewest that cover K in a given number of passes) split
+// K into 16-byte code chunks (32 codes at 4 bits, 16 at 8 bits): lane t takes the chunks t,
+// t + lanes, t + 2 lanes, ... of every one of the workgroup's columns, and loads the activations
+// of a chunk once for all COLS columns. A chunk's codes are unpacked to exact
+// 16-bit floats offset + q in K order and dotted with the activations two at a time (fp32
+// accumulate), together with the activations' sum; the group's affine terms are applied in
+// fp32 as in the staged kernel: acc += s * sum_k x_k (offset + q_k) + (b - offset * s) sum_k x_k.
+// Chunks never straddle a group (groups are 32 codes or more and chunk-aligned).
+// The lanes' partial sums are added by DPP moves within rows of 16 lanes, then across rows and
+// waves in LDS, always in the same order, so a row's result depends only on the plan (and not
+// on M or the code layout).
+#include "common.h"
+#include "affine_qmv.h"
+
+namespace mt {
+
+namespace {
+
+template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams p) {
+  constexpr int kChunks = BITS / 2;        // 16-byte chunks per column and 64-wide K step
+  constexpr int kCodes = 128 / BITS;       // codes per chunk
+  constexpr int kXLoads = kCodes / 8;      // 16-byte activation loads per chunk and row
+  constexpr int kOut = NPROJ * COLS * ROWS;
+  constexpr float kOff = CodeOffset<BITS, DT>::value;
+  __shared__ float red[kGemvMaxWaves][kOut][4];  // per wave, output and row of 16 lanes
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int waves = blockDim.x >> 6;
+  const int lanes = blockDim.x;
+  const int col0 = blockIdx.x * COLS;
+  const int M = p.M, K = p.K, N = p.N;
+  const int chunks = K / kCodes;
+  const int gshift = __builtin_ctz((unsigned)p.G);
+  const int groups_per_row = K >> gshift;
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  __amdgpu_buffer_rsrc_t rw[NPROJ], rs[NPROJ], rb[NPROJ];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr) {
+    rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * K * BITS / 8u);
+    rs[pr] = make_rsrc(p.s[pr], (uint32_t)N * groups_per_row * 2u);
+    rb[pr] = make_rsrc(p.b[pr], (uint32_t)N * groups_per_row * 2u);
+  }
+
+  struct Stage {
+    u32x4 q[NPROJ][COLS];
+    u32x4 x[ROWS][kXLoads];
+    uint32_t s[NPROJ][COLS], b[NPROJ][COLS];
+  };
+  auto load = [&](Stage& S, int kc) {
+    const bool ok = kc < chunks;
+    const int st = kc / kChunks;
+    const uint32_t wo = (uint32_t)st * p.step_stride + 16u * (uint32_t)(kc % kChunks);
+    const int k0 = kc * kCodes;
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int j = 0; j < COLS; ++j) {
+        const uint32_t col = (uint32_t)(col0 + j);
+        S.q[pr][j] = load16(rw[pr], ok ? col * p.col_stride + wo : kOOB);
+        const uint32_t go =
+            ok ? (col * (uint32_t)groups_per_row + (uint32_t)(k0 >> gshift)) * 2u : kOOB;
+        S.s[pr][j] = load2(rs[pr], go);
+        S.b[pr][j] = load2(rb[pr], go);
+      }
+#pragma unroll
+    for (int m = 0; m < ROWS; ++m)
+#pragma unroll
+      for (int v = 0; v < kXLoads; ++v)
+        S.x[m][v] = load16(rx, (ok && m < M) ? ((uint32_t)m * K + k0 + 8 * v) * 2u : kOOB);
+  };
+
+  float acc[NPROJ][COLS][ROWS];
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int j = 0; j < COLS; ++j)
+#pragma unroll
+      for (int m = 0; m < ROWS; ++m) acc[pr][j][m] = 0.0f;
+
+  auto compute = [&](const Stage& S) {
+    float xs[ROWS];
+#pragma unroll
+    for (int m = 0; m < ROWS; ++m) {
+      xs[m] = 0.0f;
+#pragma unroll
+      for (int v = 0; v < kXLoads; ++v) xs[m] = sum8<DT>(S.x[m][v], xs[m]);
+    }
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int j = 0; j < COLS; ++j) {
+        u32x4 cw[kXLoads];
+#pragma unroll
+        for (int v = 0; v < kXLoads; ++v) {
+          if constexpr (BITS == 4) {
+            cw[v] = unpack_u4<DT>(S.q[pr][j][v]);
+          } else {
+            const u32x2 lo = unpack_u8<DT>(S.q[pr][j][2 * v]);
+            const u32x2 hi = unpack_u8<DT>(S.q[pr][j][2 * v + 1]);
+            cw[v] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+          }
+        }
+        const float sf = act_to_f32<DT>(S.s[pr][j]);
+        const float bp = __builtin_fmaf(-kOff, sf, act_to_f32<DT>(S.b[pr][j]));
+#pragma unroll
+        for (int m = 0; m < ROWS; ++m) {
+          float t = 0.0f;
+#pragma unroll
+          for (int v = 0; v < kXLoads; ++v) {
+            const u32x4 xv = S.x[m][v];
+            const u32x4 cv = cw[v];
+            t = dot2<DT>(xv.x, cv.x, t);
+            t = dot2<DT>(xv.y, cv.y, t);
+            t = dot2<DT>(xv.z, cv.z, t);
+            t = dot2<DT>(xv.w, cv.w, t);
+          }
+          acc[pr][j][m] = __builtin_fmaf(sf, t, acc[pr][j][m]);
+          acc[pr][j][m] = __builtin_fmaf(bp, xs[m], acc[pr][j][m]);
+        }
+      }
+  };
+
+  // Passes of one chunk per lane, two in registers: the next pass's loads are issued before
+  // this one's math, so a workgroup with one or two passes waits for memory once. The pass
+  // count is the same for every lane (lanes past K load zeros), so the branches are uniform.
+  Stage cur, nxt;
+  load(cur, tid);
+  for (int base = 0; base < chunks; base += lanes) {
+    const bool more = base + lanes < chunks;
+    if (more) load(nxt, base + lanes + tid);
+    compute(cur);
+    if (more) cur = nxt;
+  }
+
+  // Rows of 16 lanes by DPP (each lane ends with its row's sum), then rows and waves in LDS.
+#pragma unroll
+  for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+    for (int j = 0; j < COLS; ++j)
+#pragma unroll
+      for (int m = 0; m < ROWS; ++m) {
+        float v = group_sum8(acc[pr][j][m]);
+        v += dpp_read<kDppRowRor8>(v);
+        if ((lane & 15) == 0) red[wave][(pr * COLS + j) * ROWS + m][lane >> 4] = v;
+      }
+  __syncthreads();
+  if (tid < COLS * ROWS) {
+    const int j = tid / ROWS, m = tid % ROWS;
+    float v[NPROJ];
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr) {
+      float s = 0.0f;
+      for (int w = 0; w < waves; ++w)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s += red[w][(pr * COLS + j) * ROWS + m][r];
+      v[pr] = s;
+    }
+    if (m < M) {
+      const size_t o = (size_t)m * N + col0 + j;
+      float out;
+      if constexpr (NPROJ == 2) {
+        out = silu_mul(v[0], v[1]);
+      } else {
+        out = v[0];
+        if (p.residual) out += act_to_f32<DT>(p.residual[o]);
+      }
+      p.y[o] = f32_to_act<DT>(out);
+    }
+  }
+}
+
+template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
+hipError_t launch_waves(const QmvParams& p, int waves, hipStream_t stream) {
+  affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+template <int BITS, int DT, int ROWS, int NPROJ>
+hipError_t launch_cols(const QmvParams& p, int waves, int cols, hipStream_t stream) {
+  if (cols == 2) return launch_waves<BITS, DT, ROWS, NPROJ, 2>(p, waves, stream);
+  if constexpr (affine_gemv_fits(ROWS, NPROJ, 4)) {
+    if (cols == 4) return launch_waves<BITS, DT, ROWS, NPROJ, 4>(p, waves, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+template <int BITS, int DT, int NPROJ>
+hipError_t launch_rows(const QmvParams& p, int waves, int cols, hipStream_t stream) {
+  if (p.M <= 1) return launch_cols<BITS, DT, 1, NPROJ>(p, waves, cols, stream);
+  if (p.M <= 2) return launch_cols<BITS, DT, 2, NPROJ>(p, waves, cols, stream);
+  if (p.M <= 4) return launch_cols<BITS, DT, 4, NPROJ>(p, waves, cols, stream);
+  return hipErrorInvalidValue;
+}
+
+template <int BITS, int DT>
+hipError_t launch_bits_dt(const QmvParams& p, int nproj, int waves, int cols,
+                          hipStream_t stream) {
+  return nproj == 2 ? launch_rows<BITS, DT, 2>(p, waves, cols, stream)
+                    : launch_rows<BITS, DT, 1>(p, waves, cols, stream);
+}
+
+}  // namespace
+
+hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
+                              int cols, hipStream_t stream) {
+  if (p.N % cols || p.K % 64 || p.G < 32 || !affine_gemv_fits(p.M, nproj, cols) ||
+      waves < 1 || waves > kGemvMaxWaves)
+    return hipErrorInvalidValue;
+  if (bits == 4) {
+    return dtype == kBF16 ? launch_bits_dt<4, kBF16>(p, nproj, waves, cols, stream)
+                          : launch_bits_dt<4, kF16>(p, nproj, waves, cols, stream);
+  }
+  return dtype == kBF16 ? launch_bits_dt<8, kBF16>(p, nproj, waves, cols, stream)
+                        : launch_bits_dt<8, kF16>(p, nproj, waves, cols, stream);
+}
+
+}  // namespace mt

@@ -100,6 +100,21 @@ bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size, 
 hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int nproj,
                                  hipStream_t stream);
 
+// ---- GEMV kernel (M <= 4, no K split) ----------------------------------------------------
+// Workgroups of `waves` waves (1 to kGemvMaxWaves) each own `cols` output columns (2 or 4;
+// grid N / cols) and all of K; reads x, w, s, b, residual, y, M, K, N, G and the code layout
+// of p.
+constexpr int kGemvMaxRows = 4;
+constexpr int kGemvMaxWaves = 8;
+// Whether a workgroup holds `cols` columns of `nproj` projections at `rows` rows (rounded up to
+// 1, 2 or 4) in registers: four columns of both projections above one row would spill.
+__host__ __device__ constexpr bool affine_gemv_fits(int rows, int nproj, int cols) {
+  return rows >= 1 && rows <= kGemvMaxRows && (cols == 2 || cols == 4) &&
+         (nproj == 1 || cols == 2 || rows == 1);
+}
+hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
+                              int cols, hipStream_t stream);
+
 // One-launch quantized MLP, y = down(silu(gate x) * up x) (+ residual), for M <= 16.
 // Workgroups [0, blocks_up) compute the gate/up strips of `up` (its y is the hidden
 // activation h in the workspace) and publish each finished hidden strip; the remaining

@@ -49,9 +49,9 @@ constexpr int kMaxStrips = (int)(kCounterBytes / 4);
 struct Plan {
   int ksplit;
   int steps_per_split;
-  int strips;
-  bool staged;  // activation-staged small-row kernel
-  int tiles;    // staged kernel: strips per workgroup
+  int strips;   // column strips (GEMV kernel: N / columns per workgroup)
+  int kernel;   // mt_qmv_kernel
+  int tiles;    // staged kernel: strips per workgroup; GEMV kernel: waves per workgroup
 };
 
 Plan plan_split(int K, int N) {
@@ -72,7 +72,7 @@ Plan plan_split(int K, int N) {
   p.steps_per_split = (steps + ksplit - 1) / ksplit;
   p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
   p.strips = strips;
-  p.staged = false;
+  p.kernel = MT_QMV_REGISTER;
   p.tiles = 1;
   return p;
 }
@@ -165,7 +165,7 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
     }
   }
   if (!use_lds_path(rows, plan.steps_per_split, nproj, group_size)) return plan;
-  plan.staged = true;
+  plan.kernel = MT_QMV_STAGED;
   const char* env = std::getenv("METILE_AMD_STRIPS");
   if (env && std::string(env) == "32") return plan;
   const long base = N / 32, ks = plan.ksplit;
@@ -268,27 +268,41 @@ Plan split_plan(int steps, int ksplit) {
 Plan from_public(const mt_qmv_plan& q, int K) {
   Plan p = split_plan(K / 64, q.ksplit);
   p.strips = q.strips;
-  p.staged = q.kernel == MT_QMV_STAGED;
-  p.tiles = p.staged ? q.tiles : 1;
+  p.kernel = q.kernel;
+  p.tiles = q.kernel == MT_QMV_REGISTER ? 1 : q.tiles;
   return p;
 }
 
 mt_qmv_plan to_public(const Plan& p) {
   mt_qmv_plan q{};
-  q.kernel = p.staged ? MT_QMV_STAGED : MT_QMV_REGISTER;
+  q.kernel = p.kernel;
   q.ksplit = p.ksplit;
   q.strips = p.strips;
-  q.tiles = p.staged ? p.tiles : 1;
+  q.tiles = p.kernel == MT_QMV_REGISTER ? 1 : p.tiles;
   return q;
 }
 
 // Why `q` cannot run dispatches of up to `rows` rows at this shape ("" when it can): the
 // register kernel covers 32-column strips of up to 32 rows and groups of 64 or more; the staged
 // kernel up to 16 rows, N / 32 to 2 N / 32 strips (16 to 32 columns each) in workgroups of one or
-// two strips, within its LDS; every split holds at most kMaxGroupsPerSplit - 1 groups.
+// two strips, within its LDS; every split holds at most kMaxGroupsPerSplit - 1 groups. The GEMV
+// kernel takes up to 4 rows, no K split, 2 or 4 columns per workgroup (strips = N / columns),
+// 1 to 8 waves (tiles), and not 4 columns of both projections above one row (their registers
+// spill).
 std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size,
                              const mt_qmv_plan& q) {
   const int steps = K / 64, base = N / 32;
+  if (q.kernel == MT_QMV_GEMV) {
+    if (rows > mt::kGemvMaxRows) return "more rows than the GEMV kernel takes";
+    if (q.ksplit != 1) return "the GEMV kernel does not split K";
+    if (q.strips < 1 || N % q.strips || (N / q.strips != 2 && N / q.strips != 4))
+      return "GEMV strips must be N/2 or N/4";
+    if (q.tiles < 1 || q.tiles > mt::kGemvMaxWaves)
+      return "GEMV tiles (waves per workgroup) must be in 1..8";
+    if (!mt::affine_gemv_fits(rows, nproj, N / q.strips))
+      return "the GEMV kernel does not hold this many columns and rows in registers";
+    return "";
+  }
   if (q.kernel != MT_QMV_STAGED && q.kernel != MT_QMV_REGISTER) return "unknown kernel";
   if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
   const Plan p = split_plan(steps, q.ksplit);
@@ -336,7 +350,8 @@ std::vector<int> strip_options(int N, int ksplit) {
   return out;
 }
 
-std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int group_size) {
+std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int group_size,
+                                        int bits) {
   std::vector<mt_qmv_plan> out;
   const int steps = K / 64;
   int last = 0;
@@ -352,6 +367,20 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
         if (qmv_plan_problem(rows, K, N, nproj, group_size, st).empty()) out.push_back(st);
       }
   }
+  // GEMV: for each number of passes over K (one 16-byte chunk of codes per lane and pass), the
+  // fewest waves that make it.
+  const int chunks = K * bits / 128;
+  std::vector<int> waves;
+  for (int passes = 1; passes <= 2 * mt::kGemvMaxWaves; ++passes) {
+    const int w = (chunks + 64 * passes - 1) / (64 * passes);
+    if (w <= mt::kGemvMaxWaves && (waves.empty() || waves.back() != w)) waves.push_back(w);
+    if (w == 1) break;
+  }
+  for (int cols : {4, 2})
+    for (int w : waves) {
+      const mt_qmv_plan g{MT_QMV_GEMV, 1, N / cols, w};
+      if (qmv_plan_problem(rows, K, N, nproj, group_size, g).empty()) out.push_back(g);
+    }
   return out;
 }
 
@@ -439,7 +468,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
   for (int r0 = 0; r0 < M; r0 += chunk) {
     const int rows = (M - r0) < chunk ? (M - r0) : chunk;
     const Plan plan = plan_qmv(rows, K, N, nproj, group_size, bits, dtype);
-    if (group_size == 32 && !plan.staged)
+    if (group_size == 32 && plan.kernel == MT_QMV_REGISTER)
       return fail(MT_ERR_INVALID_ARGUMENT,
                   std::string(op) + ": no staged plan fits groups of 32 at this shape");
     mt::QmvParams p{};
@@ -463,10 +492,15 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
     p.strips = plan.strips;
-    p.tiles = plan.staged ? plan.tiles : 1;
+    p.tiles = plan.kernel == MT_QMV_STAGED ? plan.tiles : 1;
     set_layout(p, layout, bits);
-    const hipError_t e = plan.staged ? mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs)
-                                     : mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
+    hipError_t e;
+    if (plan.kernel == MT_QMV_GEMV)
+      e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles, N / plan.strips, hs);
+    else if (plan.kernel == MT_QMV_STAGED)
+      e = mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs);
+    else
+      e = mt::launch_affine_qmv(p, bits, dtype, nproj, hs);
     if (e != hipSuccess) return hip_fail(e, op);
   }
   return MT_OK;
@@ -732,7 +766,8 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
                     const void* up_scales, const void* up_biases, const uint32_t* down_w,
                     const void* down_scales, const void* down_biases, const void* residual,
                     void* y, int M, int H, int I, int group_size, int bits, int dtype,
-                    void* workspace, size_t workspace_bytes, void* stream, int layout) {
+                    void* workspace, size_t workspace_bytes, void* stream, int up_layout,
+                    int down_layout) {
   int st = check_affine(op, M, H, I, group_size, bits, dtype);
   if (st) return st;
   st = check_affine(op, M, I, H, group_size, bits, dtype);
@@ -751,10 +786,10 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
     // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
     st = affine_swiglu_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
                             h, M, H, I, group_size, bits, dtype, workspace, mp.hidden, stream,
-                            layout);
+                            up_layout);
     if (st) return st;
     return affine_qmv_impl(op, h, down_w, down_scales, down_biases, residual, y, M, I, H,
-                           group_size, bits, dtype, workspace, mp.hidden, stream, layout);
+                           group_size, bits, dtype, workspace, mp.hidden, stream, down_layout);
   }
   // [counters: gate/up strips | down strips | ready[] | done][gate/up partials]
   // [down partials][hidden activation]
@@ -793,8 +828,8 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
   down.strips = strips_down;
   up.G = down.G = group_size;
   up.group_shift = down.group_shift = __builtin_ctz((unsigned)(group_size / 64));
-  set_layout(up, layout, bits);
-  set_layout(down, layout, bits);
+  set_layout(up, up_layout, bits);
+  set_layout(down, down_layout, bits);
   mt::MlpLink link{};
   link.ready = counters + strips_up + strips_down;
   link.done = link.ready + mp.down.ksplit;
@@ -854,7 +889,7 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
   return affine_mlp_impl("mt_affine_mlp", x, gate_w, gate_scales, gate_biases, up_w, up_scales,
                          up_biases, down_w, down_scales, down_biases, residual, y, M, H, I,
                          group_size, bits, dtype, workspace, workspace_bytes, stream,
-                         kLayoutMlx);
+                         kLayoutMlx, kLayoutMlx);
 }
 
 int mt_affine_quantize(const void* w, uint32_t* w_q, void* scales, void* biases, int N, int K,
@@ -927,7 +962,25 @@ int mt_affine_mlp_repacked(const void* x, const uint32_t* gate_packed, const voi
   return affine_mlp_impl("mt_affine_mlp_repacked", x, gate_packed, gate_scales, gate_biases,
                          up_packed, up_scales, up_biases, down_packed, down_scales, down_biases,
                          residual, y, M, H, I, group_size, bits, dtype, workspace,
-                         workspace_bytes, stream, kLayoutStepMajor);
+                         workspace_bytes, stream, kLayoutStepMajor, kLayoutStepMajor);
+}
+
+int mt_affine_mlp_layouts(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                          const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                          const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                          const void* down_biases, const void* residual, void* y, int M, int H,
+                          int I, int group_size, int bits, int dtype, int up_layout,
+                          int down_layout, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  for (int l : {up_layout, down_layout})
+    if (l != MT_LAYOUT_MLX && l != MT_LAYOUT_REPACKED)
+      return fail(MT_ERR_INVALID_ARGUMENT,
+                  "mt_affine_mlp_layouts: layouts must be MT_LAYOUT_MLX or MT_LAYOUT_REPACKED");
+  return affine_mlp_impl("mt_affine_mlp_layouts", x, gate_w, gate_scales, gate_biases, up_w,
+                         up_scales, up_biases, down_w, down_scales, down_biases, residual, y, M,
+                         H, I, group_size, bits, dtype, workspace, workspace_bytes, stream,
+                         up_layout == MT_LAYOUT_REPACKED ? kLayoutStepMajor : kLayoutMlx,
+                         down_layout == MT_LAYOUT_REPACKED ? kLayoutStepMajor : kLayoutMlx);
 }
 
 int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,
@@ -1059,7 +1112,8 @@ int mt_affine_qmv_plan_candidates(int M, int K, int N, int group_size, int bits,
   if (st) return st;
   if (capacity < 0 || (capacity > 0 && !out))
     return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_qmv_plan_candidates: bad output buffer");
-  const std::vector<mt_qmv_plan> c = qmv_candidates(row_bucket(M), K, N, nproj, group_size);
+  const std::vector<mt_qmv_plan> c =
+      qmv_candidates(row_bucket(M), K, N, nproj, group_size, bits);
   for (int i = 0; i < (int)c.size() && i < capacity; ++i) out[i] = c[i];
   return (int)c.size();
 }

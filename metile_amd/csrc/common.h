@@ -208,18 +208,24 @@ __device__ __forceinline__ float hi16(uint32_t w) {
   else return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
 }
 
-// acc + a.lo + a.hi for a word holding two 16-bit floats: one dot product with (1, 1), fp32
-// accumulate. The word must arrive as a scalar: with this compiler, __builtin_bit_cast applied
-// directly to an element of a vector value read the vector's first word instead (which is what
-// made dot products fed that way return wrong sums).
+// acc + a.lo * b.lo + a.hi * b.hi for words holding two 16-bit floats each, fp32 accumulate
+// (one dot-product instruction). The words must arrive as scalars: with this compiler,
+// __builtin_bit_cast applied directly to an element of a vector value read the vector's first
+// word instead (which is what made dot products fed that way return wrong sums).
 template <int DT>
-__device__ __forceinline__ float pair_sum(uint32_t a, float acc) {
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc) {
   if constexpr (DT == kBF16)
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
-                                           __builtin_bit_cast(bf16x2, 0x3f803f80u), acc, false);
+                                           __builtin_bit_cast(bf16x2, b), acc, false);
   else
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a),
-                                  __builtin_bit_cast(f16x2, 0x3c003c00u), acc, false);
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b),
+                                  acc, false);
+}
+
+// acc + a.lo + a.hi: the dot product with (1, 1).
+template <int DT>
+__device__ __forceinline__ float pair_sum(uint32_t a, float acc) {
+  return dot2<DT>(a, DT == kBF16 ? 0x3f803f80u : 0x3c003c00u, acc);
 }
 
 // Sum of the 8 16-bit floats held in a u32x4, added to acc in fp32, two per instruction.
@@ -234,6 +240,7 @@ __device__ __forceinline__ float sum8(u32x4 v, float acc) {
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
 constexpr int kDppHalfMirror = 0x141;  // row_half_mirror
+constexpr int kDppRowRor8 = 0x128;     // row_ror:8 (lane i reads lane i ^ 8 of its row)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_read(float v) {

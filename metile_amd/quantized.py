@@ -90,6 +90,10 @@ def _repacked(weight) -> bool:
     return weight.ndim == 3
 
 
+def _layout_code(weight) -> int:
+    return _lib.MT_LAYOUT_REPACKED if _repacked(weight) else _lib.MT_LAYOUT_MLX
+
+
 def _code_shape(weight, bits):
     """``(N, K)`` of packed codes in either layout, or ``None`` if the shape is neither."""
     if weight.ndim == 2:
@@ -196,14 +200,16 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
     through the workspace), two launches above that.
 
     ``gate``/``up``/``down`` are ``(weight, scales, biases)`` triples; gate/up ``[I, H]``,
-    down ``[H, I]``, all three in one code layout (MLX rows or ``affine_repack``'s). The hidden activation is rounded to the activation dtype between the two
-    projections, as the reference executor does (``metile/backends/mlx_quantized.py:1829-1830``).
+    down ``[H, I]``, gate and up in one code layout (MLX rows or ``affine_repack``'s), down in
+    either (results are the same bit for bit). The hidden activation is rounded to the
+    activation dtype between the two projections, as the reference executor does
+    (``metile/backends/mlx_quantized.py:1829-1830``).
     """
     gw, gs, gb = gate
     uw, us, ub = up
     dw, ds, db = down
-    if not (_repacked(gw) == _repacked(uw) == _repacked(dw)):
-        raise ValueError("affine MLP weights must share one code layout")
+    if _repacked(gw) != _repacked(uw):
+        raise ValueError("affine MLP gate and up weights must share one code layout")
     _require_device(values, gw, gs, gb, uw, us, ub, dw, ds, db, residual)
     code = _dtype_code(values.dtype)
     _check_params(values, gw, gs, gb, group_size, bits, "affine MLP gate")
@@ -231,10 +237,14 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
     L = _lib.lib()
     need = L.mt_affine_mlp_workspace_bytes(m, hdim, idim, group_size, bits)
     ws = workspace(values.device, need)
-    fn = L.mt_affine_mlp_repacked if _repacked(gw) else L.mt_affine_mlp
-    _lib.check(fn(
-        x.data_ptr(), *[t.data_ptr() for t in tensors], _ptr(res), out.data_ptr(), m, hdim, idim,
-        group_size, bits, code, ws.data_ptr(), ws.numel(), _stream_handle(values.device)))
+    args = (x.data_ptr(), *[t.data_ptr() for t in tensors], _ptr(res), out.data_ptr(), m, hdim,
+            idim, group_size, bits, code)
+    tail = (ws.data_ptr(), ws.numel(), _stream_handle(values.device))
+    if _repacked(gw) == _repacked(dw):
+        fn = L.mt_affine_mlp_repacked if _repacked(gw) else L.mt_affine_mlp
+        _lib.check(fn(*args, *tail))
+    else:
+        _lib.check(L.mt_affine_mlp_layouts(*args, _layout_code(gw), _layout_code(dw), *tail))
     return out
 
 
@@ -463,29 +473,30 @@ def mlx_affine_swiglu_executor(sample_values, gate_weight, gate_scales, gate_bia
     """Drop-in for ``mlx_affine_swiglu_executor`` (``metile/backends/mlx_quantized.py:1723``):
     validates once, repacks the weights ahead of time (``affine_repack``, as the reference's
     executor does for its repacked schedules, ``metile/backends/mlx_quantized.py:1082-1100``),
-    tunes the plan of the sample's shape (``metile_amd.tuning``; cached decisions are reused),
-    checks the kernel against the native composition on the sample (the reference tuner's
-    fidelity gate) and returns ``execute(values)`` bound to the repacked weights."""
+    tunes the plan of the sample's shape over both code layouts and keeps the faster
+    (``metile_amd.tuning.ensure_qmv_layout``; cached decisions are reused), checks the kernel
+    against the native composition on the sample (the reference tuner's fidelity gate) and
+    returns ``execute(values)`` bound to the kept weights."""
     from .native import native_affine_swiglu
 
     _swiglu_guards(sample_values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                    up_biases, group_size, bits)
-    gate_packed = affine_repack(gate_weight, bits=bits)
-    up_packed = affine_repack(up_weight, bits=bits)
+    mlx = (gate_weight, gate_scales, gate_biases, up_weight, up_scales, up_biases)
+    packed = (affine_repack(gate_weight, bits=bits), gate_scales, gate_biases,
+              affine_repack(up_weight, bits=bits), up_scales, up_biases)
+    kept = packed
     if autotune:
-        _tuning.ensure_qmv_plans(sample_values, (gate_packed, gate_scales, gate_biases,
-                                                 up_packed, up_scales, up_biases),
-                                 group_size=group_size, bits=bits)
+        layout = _tuning.ensure_qmv_layout(sample_values, {"repacked": packed, "mlx": mlx},
+                                           group_size=group_size, bits=bits)
+        kept = packed if layout == "repacked" else mlx
+    del packed
     _fidelity_gate(
-        affine_swiglu(sample_values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
-                      up_biases, group_size=group_size, bits=bits),
-        native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
-                             up_scales, up_biases, group_size=group_size, bits=bits),
+        affine_swiglu(sample_values, *kept, group_size=group_size, bits=bits),
+        native_affine_swiglu(sample_values, *mlx, group_size=group_size, bits=bits),
         "affine SwiGLU")
 
     def execute(values):
-        return affine_swiglu(values, gate_packed, gate_scales, gate_biases, up_packed, up_scales,
-                             up_biases, group_size=group_size, bits=bits)
+        return affine_swiglu(values, *kept, group_size=group_size, bits=bits)
 
     return execute
 
@@ -521,18 +532,27 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
                       autotune=True):
     """The steps of ``mlx_affine_mlp_executor`` after its argument checks, for weights already
     repacked: ``mlx`` and ``packed`` are the (gate, up, down) triples in MLX layout (for the
-    native compositions the gates compare against) and repacked (for the kernels). Tunes both
-    stages at the sample's shape, gates them, returns ``execute(values, residual)``."""
+    native compositions the gates compare against) and repacked. Tunes both stages at the
+    sample's shape over both code layouts, each stage keeping the layout its plan reads fastest
+    (``metile_amd.tuning.ensure_qmv_layout``; without ``autotune``, the repacked codes), gates
+    them, returns ``execute(values, residual)``."""
     from .native import native_affine_residual_qmv, native_affine_swiglu
 
-    gate, up, down = packed
     (gate_weight, gate_scales, gate_biases), (up_weight, up_scales, up_biases), \
         (down_weight, down_scales, down_biases) = mlx
+    gate, up, down = packed
     if autotune:
-        _tuning.ensure_qmv_plans(sample_values, (*gate, *up), group_size=group_size, bits=bits)
+        layout = _tuning.ensure_qmv_layout(
+            sample_values, {"repacked": (*gate, *up), "mlx": (*mlx[0], *mlx[1])},
+            group_size=group_size, bits=bits)
+        if layout == "mlx":
+            gate, up = mlx[0], mlx[1]
     hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)
     if autotune:
-        _tuning.ensure_qmv_plans(hidden, down, group_size=group_size, bits=bits)
+        layout = _tuning.ensure_qmv_layout(hidden, {"repacked": down, "mlx": mlx[2]},
+                                           group_size=group_size, bits=bits)
+        if layout == "mlx":
+            down = mlx[2]
     _fidelity_gate(
         hidden,
         native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,

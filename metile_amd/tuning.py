@@ -21,6 +21,11 @@ What differs from the reference, by design:
   the baseline (``confirm_pairwise``).
 * Every candidate's result must pass the reference tuner's fidelity gate
   (``affine_swiglu_compatible``) against the planner plan's result before it is timed.
+* A weight can be held in either code layout (MLX rows, or ``affine_repack``'s step-major
+  repack), and the fastest plan depends on it: ``ensure_qmv_layout`` measures every plan over
+  every layout the caller holds and keeps the fastest pair (the plan is installed, the layout
+  returned for the caller to keep), as the reference's executors choose between their repacked
+  and plain schedules.
 
 Environment: ``METILE_AMD_CACHE_DIR`` (cache directory), ``METILE_AMD_DISABLE_DISK_CACHE=1``
 (neither read nor write decisions), ``METILE_AMD_DISABLE_TUNING=1`` (never measure; cached
@@ -56,7 +61,9 @@ MAX_COPIES = 256
 CACHE_FILE = "affine-plans-v1.json"
 
 _LAYOUT_MLX, _LAYOUT_REPACKED = 0, 1
-_KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register"}
+_LAYOUT_NAMES = {_LAYOUT_MLX: "mlx", _LAYOUT_REPACKED: "repacked"}
+_KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register",
+            _lib.MT_QMV_GEMV: "gemv"}
 _KERNEL_CODES = {v: k for k, v in _KERNELS.items()}
 
 
@@ -129,10 +136,10 @@ def token_bucket(rows: int) -> int:
 class QmvPlan:
     """One small-row dispatch plan (``mt_qmv_plan``)."""
 
-    kernel: str  # "staged" or "register"
+    kernel: str  # "staged", "register" or "gemv"
     ksplit: int
     strips: int
-    tiles: int = 1
+    tiles: int = 1  # staged: strips per workgroup; gemv: waves per workgroup
 
     def to_c(self) -> _lib.QmvPlan:
         return _lib.QmvPlan(_KERNEL_CODES[self.kernel], self.ksplit, self.strips, self.tiles)
@@ -143,6 +150,8 @@ class QmvPlan:
 
     @property
     def workgroups(self) -> int:
+        if self.kernel == "gemv":
+            return self.strips
         return self.strips // self.tiles * self.ksplit
 
 
@@ -220,6 +229,7 @@ def clear_plans() -> None:
     with _lock:
         _lib.check(_lib.lib().mt_plans_clear())
         _decided.clear()
+        _decided_layouts.clear()
 
 
 # ---- tournament (restating metile/tuning/tournament.py:45-94) ----------------------------------
@@ -278,6 +288,7 @@ def choose(timings, baseline, cost, *, margin=SWITCH_MARGIN, tie=TIE_TOLERANCE):
 
 _lock = threading.RLock()
 _decided: dict[tuple, object] = {}
+_decided_layouts: dict[tuple, tuple] = {}
 _identity: dict[int, dict] = {}
 _BASELINE = "planner"
 
@@ -378,7 +389,7 @@ class _Bench:
         torch.cuda.synchronize(self.device)
 
 
-def _tournament(bench, graphs, copies, cost):
+def _tournament(bench, graphs, copies, cost, baseline=_BASELINE):
     """Seconds per dispatch of each key of ``graphs`` (``{key: graph}``), and the key chosen."""
     measure = bench.measure
     entries = list(graphs.items())
@@ -386,13 +397,13 @@ def _tournament(bench, graphs, copies, cost):
         measure(g)
     provisional = {k: statistics.median(v) for k, v in round_robin(entries, ROUNDS, measure).items()}
     best = min(provisional.values())
-    alternatives = [k for k in provisional if k != _BASELINE]
+    alternatives = [k for k in provisional if k != baseline]
     fastest_alt = min(alternatives, key=provisional.__getitem__) if alternatives else None
     finalists = [(k, g) for k, g in entries
-                 if provisional[k] <= best * FINALIST_SLACK or k in (_BASELINE, fastest_alt)]
-    timings = confirm_pairwise(finalists, _BASELINE, CONFIRM_ROUNDS, measure)
+                 if provisional[k] <= best * FINALIST_SLACK or k in (baseline, fastest_alt)]
+    timings = confirm_pairwise(finalists, baseline, CONFIRM_ROUNDS, measure)
     timings = {k: t / copies for k, t in timings.items()}
-    return timings, choose(timings, _BASELINE, cost)
+    return timings, choose(timings, baseline, cost)
 
 
 def _gate(result, reference, what):
@@ -405,21 +416,31 @@ def _gate(result, reference, what):
 def _tune_qmv_dispatch(values, weights, group_size, bits, layout):
     """Measure every plan of one dispatch shape (``values`` rows <= one dispatch) and return
     ``(plan or None, record)``."""
+    plan, _, record = _tune_qmv_layouts(values, [(layout, weights)], group_size, bits)
+    return plan, record
+
+
+def _tune_qmv_layouts(values, weight_sets, group_size, bits):
+    """Measure every plan of one dispatch shape over each ``(layout, weights)`` of
+    ``weight_sets`` (the same weights in different code layouts; the first is the baseline's)
+    and return ``(plan or None, layout, record)``: the fastest pair."""
     from .quantized import _as_u32
 
     L = _lib.lib()
-    nproj = len(weights) // 3
+    nproj = len(weight_sets[0][1]) // 3
     rows, k = values.shape
-    tensors = [_as_u32(t) if i % 3 == 0 else t.contiguous() for i, t in enumerate(weights)]
-    n = (tensors[0].shape[1] if layout == _LAYOUT_REPACKED else tensors[0].shape[0])
     dtype = values.dtype
     code = _dtype_code(dtype)
+    sets = []
+    for layout, weights in weight_sets:
+        tensors = [_as_u32(t) if i % 3 == 0 else t.contiguous() for i, t in enumerate(weights)]
+        sets.append((layout, tensors))
+    layout0, tensors0 = sets[0]
+    n = tensors0[0].shape[1] if layout0 == _LAYOUT_REPACKED else tensors0[0].shape[0]
     candidates = qmv_plan_candidates(rows, k, n, group_size, bits, nproj)
-    copies = _copies(_tensor_bytes(*tensors))
-    rotation = [tensors] + [[t.clone() for t in tensors] for _ in range(copies - 1)]
-    fn = ((L.mt_affine_qmv_repacked if layout == _LAYOUT_REPACKED else L.mt_affine_qmv)
-          if nproj == 1 else
-          (L.mt_affine_swiglu_repacked if layout == _LAYOUT_REPACKED else L.mt_affine_swiglu))
+    copies = _copies(_tensor_bytes(*tensors0))
+    rotations = {layout: [tensors] + [[t.clone() for t in tensors] for _ in range(copies - 1)]
+                 for layout, tensors in sets}
     need = 0
     for plan in [None, *candidates]:
         install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan)
@@ -429,42 +450,58 @@ def _tune_qmv_dispatch(values, weights, group_size, bits, layout):
     x = values.contiguous()
     outs = [torch.empty(rows, n, dtype=dtype, device=values.device) for _ in range(copies)]
 
-    def body():
-        stream = torch.cuda.current_stream(values.device).cuda_stream
-        for ts, out in zip(rotation, outs):
-            ptrs = [t.data_ptr() for t in ts]
-            if nproj == 1:
-                args = (x.data_ptr(), *ptrs, None, out.data_ptr())
-            else:
-                args = (x.data_ptr(), *ptrs, out.data_ptr())
-            _lib.check(fn(*args, rows, k, n, group_size, bits, code, bench.ws.data_ptr(),
-                          bench.ws.numel(), stream))
+    def body_for(layout):
+        fn = ((L.mt_affine_qmv_repacked if layout == _LAYOUT_REPACKED else L.mt_affine_qmv)
+              if nproj == 1 else
+              (L.mt_affine_swiglu_repacked if layout == _LAYOUT_REPACKED
+               else L.mt_affine_swiglu))
 
+        def body():
+            stream = torch.cuda.current_stream(values.device).cuda_stream
+            for ts, out in zip(rotations[layout], outs):
+                ptrs = [t.data_ptr() for t in ts]
+                if nproj == 1:
+                    args = (x.data_ptr(), *ptrs, None, out.data_ptr())
+                else:
+                    args = (x.data_ptr(), *ptrs, out.data_ptr())
+                _lib.check(fn(*args, rows, k, n, group_size, bits, code, bench.ws.data_ptr(),
+                              bench.ws.numel(), stream))
+
+        return body
+
+    baseline = (_BASELINE, layout0)
     graphs, reference = {}, None
     try:
-        for key, plan in [(_BASELINE, None), *[(c, c) for c in candidates]]:
-            install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan)
-            graphs[key] = bench.capture(body)
-            bench.stream.synchronize()
-            if reference is None:
-                reference = outs[0].clone()
-            else:
-                _gate(outs[0], reference, "affine plan tuning")
+        for layout, _ in sets:
+            body = body_for(layout)
+            for key, plan in [(_BASELINE, None), *[(c, c) for c in candidates]]:
+                install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, plan)
+                graphs[(key, layout)] = bench.capture(body)
+                bench.stream.synchronize()
+                if reference is None:
+                    reference = outs[0].clone()
+                else:
+                    _gate(outs[0], reference, "affine plan tuning")
         install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, None)
-        timings, chosen = _tournament(bench, graphs, copies,
-                                      lambda key: -1 if key == _BASELINE else key.workgroups)
+        # cost: workgroups, then the baseline's layout
+        timings, chosen = _tournament(
+            bench, graphs, copies,
+            lambda key: (-1 if key[0] == _BASELINE else key[0].workgroups, key[1] != layout0),
+            baseline)
     finally:
         install_qmv_plan(rows, k, n, group_size, bits, nproj, dtype, None)
         bench.close()
     planner = qmv_plan(rows, k, n, group_size, bits, nproj, dtype)
-    plan = None if chosen == _BASELINE else chosen
+    plan = None if chosen[0] == _BASELINE else chosen[0]
     record = {
         "planner": asdict(planner),
-        "planner_us": round(timings[_BASELINE] * 1e6, 3),
+        "planner_us": round(timings[baseline] * 1e6, 3),
         "chosen_us": round(timings[chosen] * 1e6, 3),
         "copies": copies,
     }
-    return plan, record
+    if len(sets) > 1:
+        record["layout"] = _LAYOUT_NAMES[chosen[1]]
+    return plan, chosen[1], record
 
 
 def _qmv_shape(rows, k, n, group_size, bits, nproj, dtype) -> dict:
@@ -520,6 +557,77 @@ def ensure_qmv_plans(values, weights, *, group_size, bits, autotune=True, retune
             _decided[mem] = plan
             out[rows] = plan
     return out
+
+
+_LAYOUT_CODES = {name: code for code, name in _LAYOUT_NAMES.items()}
+
+
+def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retune=False):
+    """``ensure_qmv_plans`` over one weight held in several code layouts: ``layouts`` maps
+    ``"repacked"`` and/or ``"mlx"`` to the weights (as for ``ensure_qmv_plans``) in that layout,
+    the first being the default (its planner plan is the baseline). The first dispatch shape's
+    plans are measured over every layout, which picks the plan and the layout together (plans
+    are layout-free: results are bit-identical in either layout); the other dispatch shapes are
+    then tuned in that layout. Returns the name of the layout to keep: the first when nothing
+    was measured (tuning off, or inside graph capture, with no cached decision)."""
+    names = list(layouts)
+    if not names or any(name not in _LAYOUT_CODES for name in names):
+        raise ValueError('layouts must map "repacked" and/or "mlx" to weights')
+    if len(names) == 1:
+        ensure_qmv_plans(values, layouts[names[0]], group_size=group_size, bits=bits,
+                         autotune=autotune, retune=retune)
+        return names[0]
+    from .quantized import _repacked
+
+    for name in names:
+        if _repacked(layouts[name][0]) != (name == "repacked"):
+            raise ValueError(f"the {name!r} weights are not in that layout")
+    first = layouts[names[0]]
+    nproj = len(first) // 3
+    k = values.shape[-1]
+    n = first[0].shape[1] if names[0] == "repacked" else first[0].shape[0]
+    x = values.reshape(-1, k)
+    rows = dispatch_rows(x.shape[0], group_size)[0]
+    chosen = names[0]
+    with _lock:
+        mem = ("qmv", values.device.index, token_bucket(rows), k, n, group_size, bits, nproj,
+               values.dtype)
+        lmem = (*mem, tuple(names))
+        if lmem in _decided_layouts and not retune:
+            plan, chosen = _decided_layouts[lmem]
+        else:
+            candidates = qmv_plan_candidates(rows, k, n, group_size, bits, nproj)
+            shape = _qmv_shape(rows, k, n, group_size, bits, nproj, values.dtype)
+            key = _persistent_key(values.device, "affine_qmv_layout",
+                                  {**shape, "layouts": names}, candidates)
+            found, plan, cached = (False, None, None) if retune else _read_layout_decision(key)
+            if found and cached in names:
+                chosen = cached
+            elif autotune and tuning_enabled() and not torch.cuda.is_current_stream_capturing():
+                plan, code, record = _tune_qmv_layouts(
+                    x[:rows], [(_LAYOUT_CODES[name], layouts[name]) for name in names],
+                    group_size, bits)
+                chosen = _LAYOUT_NAMES[code]
+                _write_decision(key, plan, {"op": "affine_qmv_layout", **shape,
+                                            "layouts": names, **record})
+            else:
+                found = None
+            if found is not None:
+                install_qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype, plan)
+                _decided[mem] = plan
+                _decided_layouts[lmem] = (plan, chosen)
+    ensure_qmv_plans(values, layouts[chosen], group_size=group_size, bits=bits,
+                     autotune=autotune, retune=False)
+    return chosen
+
+
+def _read_layout_decision(key):
+    """(found, plan, layout name) of a cached layout decision."""
+    found, plan = _read_decision(key, QmvPlan)
+    if not found:
+        return False, None, None
+    entry = read_json(cache_path(), {}).get(key, {})
+    return True, plan, entry.get("layout")
 
 
 def _tune_gemm(values, weight, scales, biases, group_size):

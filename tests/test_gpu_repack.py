@@ -93,6 +93,9 @@ def test_mlp_repacked_equals_native(monkeypatch, path, m):
     for _ in range(2):  # the second call finds the hand-off counters cleared again
         got = mt.affine_mlp(x, *rp, residual=r)
         assert _same(got, want)
+    # a layout per stage (mt_affine_mlp_layouts): gate/up in one, down in the other
+    assert _same(mt.affine_mlp(x, rp[0], rp[1], down, residual=r), want)
+    assert _same(mt.affine_mlp(x, gate, up, rp[2], residual=r), want)
 
 
 def test_executor_on_repacked_weights_equals_the_native_path():
@@ -105,5 +108,7 @@ def test_executor_on_repacked_weights_equals_the_native_path():
     r = act_to_torch(O.make_activations(m, h, 6, tensor_id=3), "bf16")
     ex = mt.mlx_affine_mlp_executor(x, *ts[0], *ts[1], *ts[2], r)
     assert _same(ex(x, r), mt.affine_mlp(x, *ts, residual=r))
+    ex1 = mt.mlx_affine_mlp_executor(x[:1], *ts[0], *ts[1], *ts[2], r[:1])
+    assert _same(ex1(x[:1], r[:1]), mt.affine_mlp(x[:1], *ts, residual=r[:1]))
     sw = mt.mlx_affine_swiglu_executor(x, *ts[0], *ts[1])
     assert _same(sw(x), mt.affine_swiglu(x, *ts[0], *ts[1]))

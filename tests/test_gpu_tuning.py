@@ -158,6 +158,40 @@ def test_tuner_decides_persists_and_reloads(monkeypatch, tmp_path):
     assert _same(mt.affine_swiglu(xt, *gt, *ut), mt.affine_swiglu(xt, *packed))
 
 
+def test_layout_decision_persists_and_reloads(monkeypatch, tmp_path):
+    # the down projection at M=1: plans over both code layouts, the fastest pair kept
+    monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
+    monkeypatch.delenv("METILE_AMD_DISABLE_TUNING", raising=False)
+    down = O.make_affine_weight(1536, 8960, 4, 64, 3, 14)
+    h = O.make_activations(1, 8960, 3)
+    res = O.make_activations(1, 1536, 3, tensor_id=3)
+    ref = O.affine_qmv(h, *down, 64, 4, residual=res)
+    mlx = affine_to_torch(down, "bf16")
+    packed = (mt.affine_repack(mlx[0]), mlx[1], mlx[2])
+    ht, rt = act_to_torch(h, "bf16"), act_to_torch(res, "bf16")
+    layouts = {"repacked": packed, "mlx": mlx}
+    layout = tuning.ensure_qmv_layout(ht, layouts, group_size=64, bits=4)
+    assert layout in layouts
+    entries = json.loads(tuning.cache_path().read_text())
+    assert len(entries) == 1
+    record = next(iter(entries.values()))
+    print(f"[tuner down M=1 layouts] planner {record['planner']} {record['planner_us']} us "
+          f"(repacked), chosen {record['plan']} {record['chosen_us']} us over {record['layout']}",
+          flush=True)
+    assert record["op"] == "affine_qmv_layout" and record["layout"] == layout
+    assert 0 < record["chosen_us"] <= record["planner_us"]
+    installed = tuning.qmv_plan(1, 8960, 1536, 64, 4, 1, torch.bfloat16)
+    a = mt.affine_qmv(ht, *layouts[layout], residual=rt)
+    b = mt.affine_qmv(ht, *layouts["mlx" if layout == "repacked" else "repacked"], residual=rt)
+    assert _same(a, b)
+    _check("layout-tuned down", torch_to_act(a, "bf16"), ref)
+    # a fresh process state: plan and layout come back from the cache, no measuring
+    tuning.clear_plans()
+    monkeypatch.setenv("METILE_AMD_DISABLE_TUNING", "1")
+    assert tuning.ensure_qmv_layout(ht, layouts, group_size=64, bits=4) == layout
+    assert tuning.qmv_plan(1, 8960, 1536, 64, 4, 1, torch.bfloat16) == installed
+
+
 def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
     monkeypatch.delenv("METILE_AMD_DISABLE_TUNING", raising=False)
@@ -174,6 +208,7 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     _check("tuned mlp", torch_to_act(ex(xt, rt), "bf16"), ref, min_exact=0.85)
     entries = json.loads(tuning.cache_path().read_text())
     assert {e["nproj"] for e in entries.values()} == {1, 2}  # both stages decided
+    assert all(e["layout"] in ("mlx", "repacked") for e in entries.values())
     # the prefill GEMM through the tuned reference entry
     w = affine_to_torch(O.make_affine_weight(1536, 1024, 4, 64, 9, 10), "bf16")
     aw = mt.AffineWeight.from_torch(*w)

@@ -139,10 +139,22 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
         planner = tuning.qmv_plan(rows, k, n, g, bits, nproj, dtype)
         if tuning.token_bucket(rows) == rows:
             assert planner in cands
+    gemv = [c for c in cands if c.kernel == "gemv"]
+    # GEMV plans exist for up to 4 rows: 2 and 4 columns per workgroup (4 columns of both
+    # projections only at one row), and for each number of passes over K's 16-byte chunks the
+    # fewest waves (of 64 lanes) that make it
+    bucket = tuning.token_bucket(rows)
+    cols = [2, 4] if nproj == 1 or bucket == 1 else [2]
+    chunks = k * bits // 128
+    waves = {-(-chunks // (64 * p)) for p in range(1, 17)} & set(range(1, 9))
+    assert sorted((n // c.strips, c.tiles) for c in gemv) == (
+        sorted((c, w) for c in cols for w in waves) if bucket <= 4 else [])
     for c in cands:
-        assert c.kernel in ("staged", "register")
+        assert c.kernel in ("staged", "register", "gemv")
         if c.kernel == "register":
             assert g != 32 and c.strips == n // 32 and c.tiles == 1
+        elif c.kernel == "gemv":
+            assert c.ksplit == 1 and c.workgroups == c.strips
         else:
             assert rows <= 16 and n // 32 <= c.strips <= 2 * (n // 32) and c.strips % c.tiles == 0
         tuning.install_qmv_plan(rows, k, n, g, bits, nproj, torch.bfloat16, c)
@@ -185,6 +197,10 @@ def test_installed_plans_are_bucketed_per_dtype_and_size_the_workspace(clean_pla
     (QmvPlan("staged", 0, 280, 1), "ksplit must be in 1..K/64"),
     (QmvPlan("staged", 25, 280, 1), "ksplit must be in 1..K/64"),
     (QmvPlan("staged", 7, 280, 1), "equal-length splits"),  # 24 steps in 7 splits is 6 of 4
+    (QmvPlan("gemv", 2, 2240, 4), "does not split K"),
+    (QmvPlan("gemv", 1, 1120, 4), "N/2 or N/4"),            # 8 columns per workgroup
+    (QmvPlan("gemv", 1, 2240, 0), "in 1..8"),
+    (QmvPlan("gemv", 1, 2240, 9), "in 1..8"),
 ])
 def test_invalid_qmv_plans_are_rejected(plan, message, clean_plans):
     import torch
@@ -204,6 +220,15 @@ def test_plan_rules_that_depend_on_rows_and_groups(clean_plans):
     with pytest.raises(ValueError, match="groups of 64 or more"):
         tuning.install_qmv_plan(1, 1024, 1536, 32, 8, 1, torch.bfloat16,
                                 QmvPlan("register", 1, 48, 1))
+    # the GEMV kernel takes at most 4 rows, and 4 columns of both projections at one row only
+    with pytest.raises(ValueError, match="more rows than the GEMV kernel"):
+        tuning.install_qmv_plan(5, 8960, 1536, 64, 4, 1, torch.bfloat16,
+                                QmvPlan("gemv", 1, 384, 4))
+    with pytest.raises(ValueError, match="in registers"):
+        tuning.install_qmv_plan(2, 1536, 8960, 64, 4, 2, torch.bfloat16,
+                                QmvPlan("gemv", 1, 2240, 4))
+    tuning.install_qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16, QmvPlan("gemv", 1, 2240, 4))
+    tuning.install_qmv_plan(4, 8960, 1536, 32, 8, 1, torch.bfloat16, QmvPlan("gemv", 1, 384, 8))
     # one dispatch holds at most 32 rows (16 with groups of 32)
     with pytest.raises(ValueError, match="rows of one dispatch"):
         tuning.qmv_plan(33, 1536, 8960, 64, 4, 1, torch.bfloat16)
