@@ -166,24 +166,40 @@ def choose_layout(args, values, native, packed, bits=BITS):
 # ---- sections ---------------------------------------------------------------------------------
 
 
-def section_mlp(mt, gen, device, stream, args):
+def make_stack(mt, gen, device):
+    """The 28-layer stack in MLX's layout and repacked step-major (``affine_repack``)."""
     native = [make_layer(gen, device) for _ in range(LAYERS)]
     packed = [tuple(repacked(mt, t) for t in layer) for layer in native]
     torch.cuda.synchronize()
-    # each stage's weights stay in the layout its M=1 plan reads fastest, for every row count
+    return native, packed
+
+
+def stack_layers(args, gen, device, native, packed, m):
+    """The stack as a caller serving ``m`` rows keeps it: each stage's weights in the layout its
+    plan at ``m`` rows reads fastest (``choose_layout``). Returns ``(layers, layouts)``."""
     (ng, nu, nd), (pg, pu, pd) = native[0], packed[0]
-    x1 = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
-    h1 = torch.randn(1, INTER, generator=gen, device=device).to(torch.bfloat16)
-    up_layout = choose_layout(args, x1, (*ng, *nu), (*pg, *pu))
-    down_layout = choose_layout(args, h1, nd, pd)
+    x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    up_layout = choose_layout(args, x, (*ng, *nu), (*pg, *pu))
+    from metile_amd import quantized as Q
+
+    h = Q.affine_swiglu(x, *(pg if up_layout == "repacked" else ng),
+                        *(pu if up_layout == "repacked" else nu), group_size=GROUP, bits=BITS)
+    down_layout = choose_layout(args, h, nd, pd)
     layers = [((p if up_layout == "repacked" else n)[0], (p if up_layout == "repacked" else n)[1],
                (p if down_layout == "repacked" else n)[2]) for n, p in zip(native, packed)]
-    del packed
-    kernel = {"layouts": {"gate_up": up_layout, "down": down_layout}}
+    return layers, {"gate_up": up_layout, "down": down_layout}
+
+
+def section_mlp(mt, gen, device, stream, args):
+    native, packed = make_stack(mt, gen, device)
+    kernel = {}
     wbytes = 2 * proj_weight_bytes(HIDDEN, INTER) + proj_weight_bytes(INTER, HIDDEN)
     rows_out, step_ms = {}, None
     rows = sorted({1, *(int(v) for v in args.rows.split(","))})
     for m in rows:
+        layers, layouts = stack_layers(args, gen, device, native, packed, m)
+        if m == 1:
+            kernel["layouts"] = layouts
         x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
         res = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
 
@@ -197,6 +213,7 @@ def section_mlp(mt, gen, device, stream, args):
         steps = args.steps if m == 1 else max(10, args.steps // 4)
         us = timed(stack, stream, steps, args.warmup, LAYERS)
         rows_out[str(m)] = {
+            "layouts": layouts,
             "us_per_mlp_call": round(us, 3),
             "hbm_GBps": round(mlp_bytes(m) / us / 1e3, 1),
             "weight_GBps": round(wbytes / us / 1e3, 1),
@@ -246,27 +263,26 @@ def section_mlp(mt, gen, device, stream, args):
 
 
 def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
-    """One affine projection over a rotation of distinct copies (configs 0 and 3), its codes
-    in the layout the tuner picks at the first row count."""
+    """One affine projection over a rotation of distinct copies (configs 0 and 3); at each row
+    count the codes are in the layout the tuner picks for it (both are held)."""
     wb = proj_weight_bytes(k, n, bits)
     copies = copies_for(wb)
-    ws = [make_affine(gen, device, k, n, bits) for _ in range(copies)]
-    x = torch.randn(rows[0], k, generator=gen, device=device).to(torch.bfloat16)
-    layout = choose_layout(args, x, ws[0], repacked(mt, ws[0], bits), bits)
-    if layout == "repacked":
-        ws = [repacked(mt, w, bits) for w in ws]
+    native = [make_affine(gen, device, k, n, bits) for _ in range(copies)]
+    packed = [repacked(mt, w, bits) for w in native]
     out = {}
     for m in rows:
         x = torch.randn(m, k, generator=gen, device=device).to(torch.bfloat16)
-        tune(args, x, ws[0], bits)
+        layout = choose_layout(args, x, native[0], packed[0], bits)
+        ws = packed if layout == "repacked" else native
         us = timed(lambda: [mt.affine_qmv(x, *w, group_size=GROUP, bits=bits) for w in ws],
                    stream, max(10, args.steps // 4), args.warmup, copies)
         total = wb + 2 * m * k + 2 * m * n
-        out[str(m)] = {"us": round(us, 3), "hbm_GBps": round(total / us / 1e3, 1),
+        out[str(m)] = {"layout": layout, "us": round(us, 3),
+                       "hbm_GBps": round(total / us / 1e3, 1),
                        "frac_of_peak": round(total / us / 1e3 / HBM_PEAK_GBS, 4)}
-    del ws
+    del native, packed
     return {"K": k, "N": n, "bits": bits, "group_size": GROUP, "copies": copies,
-            "layout": layout, "bytes_per_call_M1": wb + 2 * k + 2 * n, "rows": out}
+            "bytes_per_call_M1": wb + 2 * k + 2 * n, "rows": out}
 
 
 def section_dense(mt, gen, device, stream, args):
@@ -351,15 +367,17 @@ def section_ceiling(mt, device, stream, args):
 def traffic_probe(mt, gen, device, args):
     """Eager launches for the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then
     WRITE_SIZE): a plain 256 MiB device copy (the calibration kernel of known size), then the
-    headline SwiGLU and down kernels over the 28-layer stack (codes repacked, as benchmarked),
-    three passes each."""
+    headline SwiGLU and down kernels over the 28-layer stack (layouts and plans as benchmarked:
+    run with the decision cache of a tuned run and METILE_AMD_DISABLE_TUNING=1, so that no
+    candidate plan is measured here), three passes each."""
     src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(3)
     dst = torch.empty_like(src)
     for _ in range(5):
         dst.copy_(src)
     torch.cuda.synchronize()
     del src, dst
-    layers = [tuple(repacked(mt, t) for t in make_layer(gen, device)) for _ in range(LAYERS)]
+    native, packed = make_stack(mt, gen, device)
+    layers, layouts = stack_layers(args, gen, device, native, packed, 1)
     x = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
     res = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
     hs = [torch.randn(1, INTER, generator=gen, device=device).to(torch.bfloat16)
@@ -370,7 +388,8 @@ def traffic_probe(mt, gen, device, args):
         for h, (_g, _u, d) in zip(hs, layers):
             mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
     torch.cuda.synchronize()
-    print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20}), flush=True)
+    print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20, "layouts": layouts}),
+          flush=True)
 
 
 def prefill_probe(mt, gen, device):

@@ -297,9 +297,11 @@ def _device_identity(device) -> dict:
     index = device.index if device.index is not None else torch.cuda.current_device()
     if index not in _identity:
         props = torch.cuda.get_device_properties(index)
+        # (not the marketing name: it reads empty where the ids table is not found, e.g.
+        # under a profiler's preloaded runtime, which would hide every cached decision)
         _identity[index] = {
             "architecture": getattr(props, "gcnArchName", ""),
-            "device": props.name,
+            "memory_bytes": props.total_memory,
             "compute_units": props.multi_processor_count,
             "library": _lib.lib().mt_source_digest().decode(),
             "tuner_source": hashlib.sha256(Path(__file__).read_bytes()).hexdigest(),
