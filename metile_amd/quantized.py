@@ -531,28 +531,49 @@ def mlx_affine_mlp_executor(sample_values, gate_weight, gate_scales, gate_biases
 def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size=64, bits=4,
                       autotune=True):
     """The steps of ``mlx_affine_mlp_executor`` after its argument checks, for weights already
-    repacked: ``mlx`` and ``packed`` are the (gate, up, down) triples in MLX layout (for the
-    native compositions the gates compare against) and repacked. Tunes both stages at the
-    sample's shape over both code layouts, each stage keeping the layout its plan reads fastest
-    (``metile_amd.tuning.ensure_qmv_layout``; without ``autotune``, the repacked codes), gates
-    them, returns ``execute(values, residual)``."""
+    repacked: ``mlx`` and ``packed`` are the (gate, up, down) triples in MLX layout and
+    repacked. For each row bucket it serves (the sample's first, others on their first call
+    outside graph capture) both stages are tuned over both code layouts and each takes the layout
+    its plan reads fastest (``metile_amd.tuning.ensure_qmv_layout``; without ``autotune``, the
+    repacked codes): at Qwen2.5-1.5B shape, one row keeps the down projection in MLX rows and
+    two rows or more the repacked codes. Both are held (the MLX triples are the caller's). The
+    sample's results are gated against the native compositions. Returns
+    ``execute(values, residual)``."""
     from .native import native_affine_residual_qmv, native_affine_swiglu
 
     (gate_weight, gate_scales, gate_biases), (up_weight, up_scales, up_biases), \
         (down_weight, down_scales, down_biases) = mlx
-    gate, up, down = packed
-    if autotune:
+    chosen = {}  # row bucket -> (gate, up, down) in the layouts picked for it
+
+    def bucket(values):
+        rows = values.numel() // values.shape[-1]
+        return _tuning.token_bucket(_tuning.dispatch_rows(max(rows, 1), group_size)[0])
+
+    def stages(values):
+        key = bucket(values)
+        if key in chosen:
+            return chosen[key]
+        gate, up, down = packed
+        if not autotune:
+            return packed
+        if torch.cuda.is_current_stream_capturing():
+            return packed  # decided on a later call outside capture
+        x = values.reshape(-1, values.shape[-1])
         layout = _tuning.ensure_qmv_layout(
-            sample_values, {"repacked": (*gate, *up), "mlx": (*mlx[0], *mlx[1])},
+            x, {"repacked": (*gate, *up), "mlx": (*mlx[0], *mlx[1])},
             group_size=group_size, bits=bits)
         if layout == "mlx":
             gate, up = mlx[0], mlx[1]
-    hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)
-    if autotune:
+        hidden = affine_swiglu(x, *gate, *up, group_size=group_size, bits=bits)
         layout = _tuning.ensure_qmv_layout(hidden, {"repacked": down, "mlx": mlx[2]},
                                            group_size=group_size, bits=bits)
         if layout == "mlx":
             down = mlx[2]
+        chosen[key] = (gate, up, down)
+        return chosen[key]
+
+    gate, up, down = stages(sample_values)
+    hidden = affine_swiglu(sample_values, *gate, *up, group_size=group_size, bits=bits)
     _fidelity_gate(
         hidden,
         native_affine_swiglu(sample_values, gate_weight, gate_scales, gate_biases, up_weight,
@@ -565,6 +586,7 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
         "affine residual QMV")
 
     def execute(values, residual):
+        gate, up, down = stages(values)
         return affine_mlp(values, gate, up, down, group_size=group_size, bits=bits,
                           residual=residual)
 

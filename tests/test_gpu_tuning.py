@@ -209,6 +209,11 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     entries = json.loads(tuning.cache_path().read_text())
     assert {e["nproj"] for e in entries.values()} == {1, 2}  # both stages decided
     assert all(e["layout"] in ("mlx", "repacked") for e in entries.values())
+    # a one-row call: its row bucket gets its own plans and layouts on first use
+    ref1, _ = O.affine_mlp(x[:1], gate, up, down, 64, 4, residual=res[:1])
+    _check("tuned mlp, one row", torch_to_act(ex(xt[:1], rt[:1]), "bf16"), ref1, min_exact=0.85)
+    rows = {(e["rows"], e["nproj"]) for e in json.loads(tuning.cache_path().read_text()).values()}
+    assert {(1, 1), (1, 2), (4, 1), (4, 2)} <= rows
     # the prefill GEMM through the tuned reference entry
     w = affine_to_torch(O.make_affine_weight(1536, 1024, 4, 64, 9, 10), "bf16")
     aw = mt.AffineWeight.from_torch(*w)
