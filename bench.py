@@ -190,6 +190,22 @@ def stack_layers(args, gen, device, native, packed, m):
     return layers, {"gate_up": up_layout, "down": down_layout}
 
 
+def kernel_label(k, n, nproj):
+    """The kernel instance an M=1 dispatch of this shape runs under the plan installed now."""
+    from metile_amd import tuning
+
+    plan = tuning.qmv_plan(1, k, n, GROUP, BITS, nproj, torch.bfloat16)
+    if plan.kernel == "gemv":
+        cols, waves = n // plan.strips, plan.tiles
+        one_pass = "true" if k * BITS // 128 <= 64 * waves else "false"
+        return (f"affine_gemv_kernel<{BITS}, 0, 1, {nproj}, {cols}, {one_pass}> "
+                f"({plan.strips} workgroups of {waves} waves)")
+    if plan.kernel == "staged":
+        return (f"affine_qmv_lds_kernel<{BITS}, 0, 8, {nproj}, ...> "
+                f"({plan.strips} strips, {plan.ksplit} K splits)")
+    return f"affine_qmv_kernel<{BITS}, 0, ..., {nproj}, ...> ({plan.ksplit} K splits)"
+
+
 def section_mlp(mt, gen, device, stream, args):
     native, packed = make_stack(mt, gen, device)
     kernel = {}
@@ -232,6 +248,8 @@ def section_mlp(mt, gen, device, stream, args):
                 return [mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
                         for h, (_g, _u, d) in zip(hs, layers)]
 
+            kernel["swiglu_label"] = kernel_label(HIDDEN, INTER, 2)
+            kernel["down_label"] = kernel_label(INTER, HIDDEN, 1)
             kernel["swiglu_us"] = timed(swiglu, stream, args.steps, args.warmup, LAYERS)
             kernel["down_us"] = timed(down, stream, args.steps, args.warmup, LAYERS)
             kernel["swiglu_bytes"] = (2 * proj_weight_bytes(HIDDEN, INTER) + 2 * m * HIDDEN
@@ -559,7 +577,8 @@ def main():
         "rows": rows_out,
         "roofline": {
             "bound": "hbm",
-            "kernel": "affine_qmv_lds_kernel<4, 0, 8, 2, 3, false, 1> (fused gate/up SwiGLU), M=1",
+            "kernel": kernel["swiglu_label"] + " (fused gate/up SwiGLU), M=1",
+            "down_kernel": kernel["down_label"],
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

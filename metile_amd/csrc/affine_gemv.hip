@@ -34,7 +34,9 @@ __device__ __forceinline__ int gemv_column_group(int b, int groups) {
   return (b % kXcds) * (whole / kXcds) + b / kXcds;
 }
 
-template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
+// ONE_PASS: every lane has at most one chunk per column (K / chunk <= lanes), so no second
+// pass is held in registers (more waves fit on a CU).
+template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams p) {
   constexpr int kChunks = BITS / 2;        // 16-byte chunks per column and 64-wide K step
   constexpr int kCodes = 128 / BITS;       // codes per chunk
@@ -145,13 +147,19 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   // Passes of one chunk per lane, two in registers: the next pass's loads are issued before
   // this one's math, so a workgroup with one or two passes waits for memory once. The pass
   // count is the same for every lane (lanes past K load zeros), so the branches are uniform.
-  Stage cur, nxt;
-  load(cur, tid);
-  for (int base = 0; base < chunks; base += lanes) {
-    const bool more = base + lanes < chunks;
-    if (more) load(nxt, base + lanes + tid);
+  if constexpr (ONE_PASS) {
+    Stage cur;
+    load(cur, tid);
     compute(cur);
-    if (more) cur = nxt;
+  } else {
+    Stage cur, nxt;
+    load(cur, tid);
+    for (int base = 0; base < chunks; base += lanes) {
+      const bool more = base + lanes < chunks;
+      if (more) load(nxt, base + lanes + tid);
+      compute(cur);
+      if (more) cur = nxt;
+    }
   }
 
   // Rows of 16 lanes by DPP (each lane ends with its row's sum), then rows and waves in LDS.
@@ -193,7 +201,11 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 
 template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
 hipError_t launch_waves(const QmvParams& p, int waves, hipStream_t stream) {
-  affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
+  const int chunks = p.K * BITS / 128;
+  if (chunks <= 64 * waves)
+    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
+  else
+    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
   return hipGetLastError();
 }
 
