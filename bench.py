@@ -422,7 +422,7 @@ def prefill_probe(mt, gen, device):
 
 
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "affine_qmv_lds_swiglu_m1_hbm_traffic.md")
+                               "affine_swiglu_m1_hbm_traffic.md")
 
 
 def measured_traffic():

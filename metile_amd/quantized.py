@@ -535,8 +535,9 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
     repacked. For each row bucket it serves (the sample's first, others on their first call
     outside graph capture) both stages are tuned over both code layouts and each takes the layout
     its plan reads fastest (``metile_amd.tuning.ensure_qmv_layout``; without ``autotune``, the
-    repacked codes): at Qwen2.5-1.5B shape, one row keeps the down projection in MLX rows and
-    two rows or more the repacked codes. Both are held (the MLX triples are the caller's). The
+    repacked codes): at Qwen2.5-1.5B shape, one row keeps both stages in MLX rows (GEMV
+    kernel), four rows or more the repacked codes. Both are held (the MLX triples are the
+    caller's). The
     sample's results are gated against the native compositions. Returns
     ``execute(values, residual)``."""
     from .native import native_affine_residual_qmv, native_affine_swiglu
