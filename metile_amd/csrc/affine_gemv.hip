@@ -201,20 +201,21 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 
 template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
 hipError_t launch_waves(const QmvParams& p, int waves, hipStream_t stream) {
-  const int chunks = p.K * BITS / 128;
-  if (chunks <= 64 * waves)
+  if (affine_gemv_one_pass(p.K, BITS, waves)) {
     affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
-  else
+    return hipGetLastError();
+  }
+  if constexpr (affine_gemv_fits(ROWS, NPROJ, COLS, false)) {
     affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
-  return hipGetLastError();
+    return hipGetLastError();
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int BITS, int DT, int ROWS, int NPROJ>
 hipError_t launch_cols(const QmvParams& p, int waves, int cols, hipStream_t stream) {
   if (cols == 2) return launch_waves<BITS, DT, ROWS, NPROJ, 2>(p, waves, stream);
-  if constexpr (affine_gemv_fits(ROWS, NPROJ, 4)) {
-    if (cols == 4) return launch_waves<BITS, DT, ROWS, NPROJ, 4>(p, waves, stream);
-  }
+  if (cols == 4) return launch_waves<BITS, DT, ROWS, NPROJ, 4>(p, waves, stream);
   return hipErrorInvalidValue;
 }
 
@@ -237,8 +238,8 @@ hipError_t launch_bits_dt(const QmvParams& p, int nproj, int waves, int cols,
 
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream) {
-  if (p.N % cols || p.K % 64 || p.G < 32 || !affine_gemv_fits(p.M, nproj, cols) ||
-      waves < 1 || waves > kGemvMaxWaves)
+  if (p.N % cols || p.K % 64 || p.G < 32 || waves < 1 || waves > kGemvMaxWaves ||
+      !affine_gemv_fits(p.M, nproj, cols, affine_gemv_one_pass(p.K, bits, waves)))
     return hipErrorInvalidValue;
   if (bits == 4) {
     return dtype == kBF16 ? launch_bits_dt<4, kBF16>(p, nproj, waves, cols, stream)

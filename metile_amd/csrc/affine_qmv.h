@@ -107,10 +107,19 @@ hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int np
 constexpr int kGemvMaxRows = 4;
 constexpr int kGemvMaxWaves = 8;
 // Whether a workgroup holds `cols` columns of `nproj` projections at `rows` rows (rounded up to
-// 1, 2 or 4) in registers: four columns of both projections above one row would spill.
-__host__ __device__ constexpr bool affine_gemv_fits(int rows, int nproj, int cols) {
+// 1, 2 or 4) in registers without spilling: always when every lane has one chunk per column
+// (`one_pass`: one pass of loads in registers), else (two passes) when nproj * cols * rows <= 8.
+__host__ __device__ constexpr int affine_gemv_row_bucket(int rows) {
+  return rows <= 1 ? 1 : rows <= 2 ? 2 : 4;
+}
+__host__ __device__ constexpr bool affine_gemv_fits(int rows, int nproj, int cols,
+                                                    bool one_pass) {
   return rows >= 1 && rows <= kGemvMaxRows && (cols == 2 || cols == 4) &&
-         (nproj == 1 || cols == 2 || rows == 1);
+         (one_pass || nproj * cols * affine_gemv_row_bucket(rows) <= 8);
+}
+// Whether a dispatch of K codes per column takes one pass with `waves` waves.
+__host__ __device__ constexpr bool affine_gemv_one_pass(int K, int bits, int waves) {
+  return K * bits / 128 <= 64 * waves;
 }
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream);

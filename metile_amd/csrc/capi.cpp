@@ -287,9 +287,9 @@ mt_qmv_plan to_public(const Plan& p) {
 // kernel up to 16 rows, N / 32 to 2 N / 32 strips (16 to 32 columns each) in workgroups of one or
 // two strips, within its LDS; every split holds at most kMaxGroupsPerSplit - 1 groups. The GEMV
 // kernel takes up to 4 rows, no K split, 2 or 4 columns per workgroup (strips = N / columns),
-// 1 to 8 waves (tiles), and not 4 columns of both projections above one row (their registers
-// spill).
-std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size,
+// 1 to 8 waves (tiles), and when a lane has more than one chunk per column, at most 8 of
+// projections x columns x rows (more would spill registers).
+std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, int bits,
                              const mt_qmv_plan& q) {
   const int steps = K / 64, base = N / 32;
   if (q.kernel == MT_QMV_GEMV) {
@@ -299,7 +299,8 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size,
       return "GEMV strips must be N/2 or N/4";
     if (q.tiles < 1 || q.tiles > mt::kGemvMaxWaves)
       return "GEMV tiles (waves per workgroup) must be in 1..8";
-    if (!mt::affine_gemv_fits(rows, nproj, N / q.strips))
+    if (!mt::affine_gemv_fits(rows, nproj, N / q.strips,
+                              mt::affine_gemv_one_pass(K, bits, q.tiles)))
       return "the GEMV kernel does not hold this many columns and rows in registers";
     return "";
   }
@@ -360,11 +361,11 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
     if (p.ksplit == last) continue;
     last = p.ksplit;
     const mt_qmv_plan reg{MT_QMV_REGISTER, p.ksplit, N / 32, 1};
-    if (qmv_plan_problem(rows, K, N, nproj, group_size, reg).empty()) out.push_back(reg);
+    if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, reg).empty()) out.push_back(reg);
     for (int strips : strip_options(N, p.ksplit))
       for (int tiles : {1, 2}) {
         const mt_qmv_plan st{MT_QMV_STAGED, p.ksplit, strips, tiles};
-        if (qmv_plan_problem(rows, K, N, nproj, group_size, st).empty()) out.push_back(st);
+        if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, st).empty()) out.push_back(st);
       }
   }
   // GEMV: for each number of passes over K (one 16-byte chunk of codes per lane and pass), the
@@ -379,7 +380,7 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
   for (int cols : {4, 2})
     for (int w : waves) {
       const mt_qmv_plan g{MT_QMV_GEMV, 1, N / cols, w};
-      if (qmv_plan_problem(rows, K, N, nproj, group_size, g).empty()) out.push_back(g);
+      if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
     }
   return out;
 }
@@ -1125,7 +1126,7 @@ int mt_affine_qmv_plan_set(int M, int K, int N, int group_size, int bits, int np
   if (st) return st;
   const PlanKey key = qmv_key(M, K, N, nproj, group_size, bits, dtype);
   if (plan) {
-    const std::string why = qmv_plan_problem(key.rows, K, N, nproj, group_size, *plan);
+    const std::string why = qmv_plan_problem(key.rows, K, N, nproj, group_size, bits, *plan);
     if (!why.empty()) return fail(MT_ERR_INVALID_ARGUMENT, "mt_affine_qmv_plan_set: " + why);
   }
   std::unique_lock<std::shared_mutex> lock(g_plans_mu);

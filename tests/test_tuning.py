@@ -140,15 +140,18 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
         if tuning.token_bucket(rows) == rows:
             assert planner in cands
     gemv = [c for c in cands if c.kernel == "gemv"]
-    # GEMV plans exist for up to 4 rows: 2 and 4 columns per workgroup (4 columns of both
-    # projections only at one row), and for each number of passes over K's 16-byte chunks the
-    # fewest waves (of 64 lanes) that make it
+    # GEMV plans exist for up to 4 rows: 2 and 4 columns per workgroup, and for each number of
+    # passes over K's 16-byte chunks the fewest waves (of 64 lanes) that make it; with more
+    # than one pass, at most 8 of projections x columns x rows (registers)
     bucket = tuning.token_bucket(rows)
-    cols = [2, 4] if nproj == 1 or bucket == 1 else [2]
     chunks = k * bits // 128
     waves = {-(-chunks // (64 * p)) for p in range(1, 17)} & set(range(1, 9))
+
+    def fits(c, w):
+        return chunks <= 64 * w or nproj * c * min(bucket, 4) <= 8
+
     assert sorted((n // c.strips, c.tiles) for c in gemv) == (
-        sorted((c, w) for c in cols for w in waves) if bucket <= 4 else [])
+        sorted((c, w) for c in (2, 4) for w in waves if fits(c, w)) if bucket <= 4 else [])
     for c in cands:
         assert c.kernel in ("staged", "register", "gemv")
         if c.kernel == "register":
@@ -220,15 +223,17 @@ def test_plan_rules_that_depend_on_rows_and_groups(clean_plans):
     with pytest.raises(ValueError, match="groups of 64 or more"):
         tuning.install_qmv_plan(1, 1024, 1536, 32, 8, 1, torch.bfloat16,
                                 QmvPlan("register", 1, 48, 1))
-    # the GEMV kernel takes at most 4 rows, and 4 columns of both projections at one row only
+    # the GEMV kernel takes at most 4 rows; with two passes over K (280 chunks per column, 128
+    # lanes) at most 8 of projections x columns x rows; in one pass (48 chunks) any
     with pytest.raises(ValueError, match="more rows than the GEMV kernel"):
         tuning.install_qmv_plan(5, 8960, 1536, 64, 4, 1, torch.bfloat16,
                                 QmvPlan("gemv", 1, 384, 4))
     with pytest.raises(ValueError, match="in registers"):
-        tuning.install_qmv_plan(2, 1536, 8960, 64, 4, 2, torch.bfloat16,
-                                QmvPlan("gemv", 1, 2240, 4))
-    tuning.install_qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16, QmvPlan("gemv", 1, 2240, 4))
-    tuning.install_qmv_plan(4, 8960, 1536, 32, 8, 1, torch.bfloat16, QmvPlan("gemv", 1, 384, 8))
+        tuning.install_qmv_plan(4, 8960, 1536, 64, 4, 1, torch.bfloat16,
+                                QmvPlan("gemv", 1, 384, 2))
+    tuning.install_qmv_plan(4, 8960, 1536, 64, 4, 1, torch.bfloat16, QmvPlan("gemv", 1, 768, 2))
+    tuning.install_qmv_plan(4, 1536, 8960, 64, 4, 2, torch.bfloat16, QmvPlan("gemv", 1, 2240, 1))
+    tuning.install_qmv_plan(4, 8960, 1536, 32, 8, 1, torch.bfloat16, QmvPlan("gemv", 1, 768, 8))
     # one dispatch holds at most 32 rows (16 with groups of 32)
     with pytest.raises(ValueError, match="rows of one dispatch"):
         tuning.qmv_plan(33, 1536, 8960, 64, 4, 1, torch.bfloat16)
