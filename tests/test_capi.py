@@ -66,3 +66,17 @@ def test_repack_argument_checks_without_gpu():
     assert lib.mt_affine_repack(ctypes.c_void_p(264), buf, 16, 128, 4, None) == \
         _lib.MT_ERR_INVALID_ARGUMENT
     assert "aligned" in lib.mt_last_error().decode()
+
+
+def test_mlp_layouts_argument_checks_without_gpu():
+    lib = _lib.lib()
+    args = [None] * 12 + [1, 1536, 8960, 64, 4, 0]
+    # an unknown layout is refused before anything else is read
+    for up, down in ((2, 0), (0, -1)):
+        st = lib.mt_affine_mlp_layouts(*args, up, down, None, 0, None)
+        assert st == _lib.MT_ERR_INVALID_ARGUMENT
+        assert "MT_LAYOUT_MLX or MT_LAYOUT_REPACKED" in lib.mt_last_error().decode()
+    # valid layouts reach the usual shape and pointer checks
+    st = lib.mt_affine_mlp_layouts(*args, _lib.MT_LAYOUT_REPACKED, _lib.MT_LAYOUT_MLX, None, 0,
+                                   None)
+    assert st != 0 and "LAYOUT" not in lib.mt_last_error().decode()

@@ -287,3 +287,19 @@ def test_library_reports_the_digest_of_its_sources():
     if max(p.stat().st_mtime for p in sources) > build.LIB.stat().st_mtime:
         pytest.skip("a source changed after the library was built: rebuild to compare digests")
     assert digest == build.source_digest()
+
+
+def test_layout_choice_argument_checks():
+    # the layout map is validated before anything is measured (no GPU needed)
+    import torch
+
+    x = torch.zeros(1, 128, dtype=torch.bfloat16)
+    mlx = (torch.zeros(64, 16, dtype=torch.int32), torch.zeros(64, 2, dtype=torch.bfloat16),
+           torch.zeros(64, 2, dtype=torch.bfloat16))
+    packed = (torch.zeros(2, 64, 8, dtype=torch.int32), mlx[1], mlx[2])
+    with pytest.raises(ValueError, match="layouts must map"):
+        tuning.ensure_qmv_layout(x, {}, group_size=64, bits=4)
+    with pytest.raises(ValueError, match="layouts must map"):
+        tuning.ensure_qmv_layout(x, {"packed": packed, "mlx": mlx}, group_size=64, bits=4)
+    with pytest.raises(ValueError, match="not in that layout"):
+        tuning.ensure_qmv_layout(x, {"repacked": mlx, "mlx": packed}, group_size=64, bits=4)
