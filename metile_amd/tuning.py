@@ -603,7 +603,8 @@ def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retun
             key = _persistent_key(values.device, "affine_qmv_layout",
                                   {**shape, "layouts": names}, candidates)
             found, plan, cached = (False, None, None) if retune else _read_layout_decision(key)
-            if found and cached in names:
+            decided = found and cached in names
+            if decided:
                 chosen = cached
             elif autotune and tuning_enabled() and not torch.cuda.is_current_stream_capturing():
                 plan, code, record = _tune_qmv_layouts(
@@ -612,9 +613,8 @@ def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retun
                 chosen = _LAYOUT_NAMES[code]
                 _write_decision(key, plan, {"op": "affine_qmv_layout", **shape,
                                             "layouts": names, **record})
-            else:
-                found = None
-            if found is not None:
+                decided = True
+            if decided:
                 install_qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype, plan)
                 _decided[mem] = plan
                 _decided_layouts[lmem] = (plan, chosen)
