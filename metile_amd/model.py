@@ -152,16 +152,22 @@ _quantized_mlp_executor_cache: dict[int, tuple] = {}
 
 
 def _execute_quantized_mlp(module, values, residual=None):
-    """Without a residual: the fused gate/up SwiGLU kernel on the shape's tuned plan (the
-    reference calls its tuned ``mlx_affine_swiglu`` here), then the module's down projection.
+    """Without a residual: the fused gate/up SwiGLU kernel on the shape's tuned plan, over the
+    code layout (MLX rows or repacked, both held by ``QuantizedLinear``) that plan reads fastest
+    (the reference calls its tuned ``mlx_affine_swiglu`` here), then the module's down projection.
     With one: ``down(swiglu(values)) + residual`` through an MLP executor bound to this module's
     repacked codes, created (tuned, fidelity-gated) on first use and cached while the module
     lives (``metile/integrations/mlx_lm.py:3837-3886``)."""
     gate, up = module.gate_proj, module.up_proj
     if residual is None:
-        weights = (gate.packed, gate.scales, gate.biases, up.packed, up.scales, up.biases)
-        _tuning.ensure_qmv_plans(values, weights, group_size=gate.group_size, bits=gate.bits)
-        hidden = affine_swiglu(values, *weights, group_size=gate.group_size, bits=gate.bits)
+        layouts = {"repacked": (gate.packed, gate.scales, gate.biases,
+                                up.packed, up.scales, up.biases),
+                   "mlx": (gate.weight, gate.scales, gate.biases,
+                           up.weight, up.scales, up.biases)}
+        layout = _tuning.ensure_qmv_layout(values, layouts, group_size=gate.group_size,
+                                           bits=gate.bits)
+        hidden = affine_swiglu(values, *layouts[layout], group_size=gate.group_size,
+                               bits=gate.bits)
         return module.down_proj(hidden)
     key = id(module)
     cached = _quantized_mlp_executor_cache.get(key)

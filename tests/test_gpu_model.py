@@ -18,6 +18,8 @@
 
 from __future__ import annotations
 
+import json
+
 import numpy as np
 import pytest
 import torch
@@ -197,3 +199,23 @@ def test_prefill_rows_take_the_gemm_and_match_the_decode_path():
             mt.restore_patches(replacements)
     scale = float(base.abs().max())
     assert float((fused - base).abs().max()) <= LOGIT_TOLERANCE * scale
+
+
+def test_tuned_graph_fusion_decodes_the_same_tokens(monkeypatch, tmp_path):
+    # with the tuner on, the MLP executors pick plans and code layouts per row bucket (the
+    # prompt's 12 rows, then one row per decode step); the tokens must still match
+    monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
+    monkeypatch.delenv("METILE_AMD_DISABLE_TUNING", raising=False)
+    from metile_amd import tuning
+
+    tuning.clear_plans()
+    try:
+        model = _tiny_model("qwen2")
+        base, patched, calls = _decode_patched(model, mt.patch_graph_fusion,
+                                               "_execute_quantized_mlp")
+        assert calls == {"plain": 0, "residual": 3 * 25}
+        decisions = json.loads(tuning.cache_path().read_text()).values()
+        assert {(d["rows"], d["nproj"]) for d in decisions} >= {(1, 1), (1, 2), (16, 1), (16, 2)}
+        _assert_same_decode("qwen2 tuned", base, patched)
+    finally:
+        tuning.clear_plans()
