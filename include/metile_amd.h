@@ -191,8 +191,10 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
 /* How one small-row dispatch runs: the kernel, the number of K splits, the number of column
  * strips (workgroup columns; N/32 for the register kernel, N/32 to 2N/32 for the staged kernel)
  * and the strips per workgroup (1 or 2, staged kernel only). The GEMV kernel (up to 4 rows)
- * never splits K: its strips are N/4 or N/2 (4 or 2 columns per workgroup) and `tiles` holds
- * its waves per workgroup (2, 4 or 8). */
+ * never splits K: its strips are N/4 or N/2 (4 or 2 columns per workgroup), `tiles` holds its
+ * waves per workgroup (1 to 8) and `order` how workgroups take column groups (0: in index
+ * order; 1: dealt out to the 8 XCDs in runs of adjacent groups). `order` is 0 for the other
+ * kernels. */
 typedef enum mt_qmv_kernel {
   MT_QMV_STAGED = 1,
   MT_QMV_REGISTER = 2,
@@ -203,6 +205,7 @@ typedef struct mt_qmv_plan {
   int ksplit;
   int strips;
   int tiles;
+  int order;
 } mt_qmv_plan;
 
 /* How the prefill GEMM runs: output tiles of tile x tile (64 or 128) and K splits. */

@@ -31,7 +31,7 @@ class QmvPlan(ctypes.Structure):
     """``mt_qmv_plan``."""
 
     _fields_ = [("kernel", ctypes.c_int), ("ksplit", ctypes.c_int), ("strips", ctypes.c_int),
-                ("tiles", ctypes.c_int)]
+                ("tiles", ctypes.c_int), ("order", ctypes.c_int)]
 
 
 class GemmPlan(ctypes.Structure):

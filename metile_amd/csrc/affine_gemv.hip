@@ -22,11 +22,13 @@ namespace mt {
 
 namespace {
 
-// Column group of workgroup b: consecutive workgroups are dispatched to the 8 XCDs in turn, so
-// the groups are dealt out XCD by XCD (workgroups b, b + 8, b + 16, ... take adjacent column
-// groups), and neighbouring columns share their XCD's L2 for the cache lines they have in
-// common (scale and bias rows do not start on line boundaries). Any order is correct; this one
-// only saves fetches. Groups past the last multiple of 8 keep their index.
+// Column group of workgroup b under plan order 1: consecutive workgroups are dispatched to the
+// 8 XCDs in turn, so the groups are dealt out XCD by XCD (workgroups b, b + 8, b + 16, ... take
+// adjacent column groups), and neighbouring columns share their XCD's L2 for the cache lines
+// they have in common (scale and bias rows do not start on line boundaries). Any order is
+// correct; which is faster depends on the shape (measured: the one-row down projection 4.41 ->
+// 4.30 us with this order, the one-row SwiGLU 6.99 -> 7.14 us), so the plan picks it. Groups
+// past the last multiple of 8 keep their index.
 __device__ __forceinline__ int gemv_column_group(int b, int groups) {
   constexpr int kXcds = 8;
   const int whole = groups - groups % kXcds;
@@ -50,7 +52,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   const int wave = tid >> 6;
   const int waves = blockDim.x >> 6;
   const int lanes = blockDim.x;
-  const int col0 = gemv_column_group(blockIdx.x, gridDim.x) * COLS;
+  const int col0 = (p.order ? gemv_column_group(blockIdx.x, gridDim.x) : blockIdx.x) * COLS;
   const int M = p.M, K = p.K, N = p.N;
   const int chunks = K / kCodes;
   const int gshift = __builtin_ctz((unsigned)p.G);

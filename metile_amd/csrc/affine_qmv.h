@@ -34,6 +34,7 @@ struct QmvParams {
   uint32_t step_stride;
   int col_align;             // staged kernels: strip boundaries at multiples of this many
                              // columns (1, or a 128-byte line of repacked codes)
+  int order;                 // GEMV kernel: 1 = column groups dealt out XCD by XCD
 };
 
 // Step-major repack of MLX affine codes: the 8 * bits bytes of column n and K step t (codes

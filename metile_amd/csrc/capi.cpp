@@ -52,6 +52,7 @@ struct Plan {
   int strips;   // column strips (GEMV kernel: N / columns per workgroup)
   int kernel;   // mt_qmv_kernel
   int tiles;    // staged kernel: strips per workgroup; GEMV kernel: waves per workgroup
+  int order;    // GEMV kernel: workgroup order (mt_qmv_plan.order)
 };
 
 Plan plan_split(int K, int N) {
@@ -74,6 +75,7 @@ Plan plan_split(int K, int N) {
   p.strips = strips;
   p.kernel = MT_QMV_REGISTER;
   p.tiles = 1;
+  p.order = 0;
   return p;
 }
 
@@ -270,6 +272,7 @@ Plan from_public(const mt_qmv_plan& q, int K) {
   p.strips = q.strips;
   p.kernel = q.kernel;
   p.tiles = q.kernel == MT_QMV_REGISTER ? 1 : q.tiles;
+  p.order = q.kernel == MT_QMV_GEMV ? q.order : 0;
   return p;
 }
 
@@ -279,6 +282,7 @@ mt_qmv_plan to_public(const Plan& p) {
   q.ksplit = p.ksplit;
   q.strips = p.strips;
   q.tiles = p.kernel == MT_QMV_REGISTER ? 1 : p.tiles;
+  q.order = p.kernel == MT_QMV_GEMV ? p.order : 0;
   return q;
 }
 
@@ -299,12 +303,14 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
       return "GEMV strips must be N/2 or N/4";
     if (q.tiles < 1 || q.tiles > mt::kGemvMaxWaves)
       return "GEMV tiles (waves per workgroup) must be in 1..8";
+    if (q.order != 0 && q.order != 1) return "GEMV order must be 0 or 1";
     if (!mt::affine_gemv_fits(rows, nproj, N / q.strips,
                               mt::affine_gemv_one_pass(K, bits, q.tiles)))
       return "the GEMV kernel does not hold this many columns and rows in registers";
     return "";
   }
   if (q.kernel != MT_QMV_STAGED && q.kernel != MT_QMV_REGISTER) return "unknown kernel";
+  if (q.order != 0) return "order is a GEMV plan field (0 for the other kernels)";
   if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
   const Plan p = split_plan(steps, q.ksplit);
   if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
@@ -360,11 +366,11 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
     const Plan p = split_plan(steps, ks);
     if (p.ksplit == last) continue;
     last = p.ksplit;
-    const mt_qmv_plan reg{MT_QMV_REGISTER, p.ksplit, N / 32, 1};
+    const mt_qmv_plan reg{MT_QMV_REGISTER, p.ksplit, N / 32, 1, 0};
     if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, reg).empty()) out.push_back(reg);
     for (int strips : strip_options(N, p.ksplit))
       for (int tiles : {1, 2}) {
-        const mt_qmv_plan st{MT_QMV_STAGED, p.ksplit, strips, tiles};
+        const mt_qmv_plan st{MT_QMV_STAGED, p.ksplit, strips, tiles, 0};
         if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, st).empty()) out.push_back(st);
       }
   }
@@ -378,10 +384,11 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
     if (w == 1) break;
   }
   for (int cols : {4, 2})
-    for (int w : waves) {
-      const mt_qmv_plan g{MT_QMV_GEMV, 1, N / cols, w};
-      if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
-    }
+    for (int w : waves)
+      for (int order : {1, 0}) {
+        const mt_qmv_plan g{MT_QMV_GEMV, 1, N / cols, w, order};
+        if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
+      }
   return out;
 }
 
@@ -494,6 +501,7 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.steps_per_split = plan.steps_per_split;
     p.strips = plan.strips;
     p.tiles = plan.kernel == MT_QMV_STAGED ? plan.tiles : 1;
+    p.order = plan.order;
     set_layout(p, layout, bits);
     hipError_t e;
     if (plan.kernel == MT_QMV_GEMV)

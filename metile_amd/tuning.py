@@ -140,13 +140,15 @@ class QmvPlan:
     ksplit: int
     strips: int
     tiles: int = 1  # staged: strips per workgroup; gemv: waves per workgroup
+    order: int = 0  # gemv: 0 index order, 1 column groups dealt out XCD by XCD
 
     def to_c(self) -> _lib.QmvPlan:
-        return _lib.QmvPlan(_KERNEL_CODES[self.kernel], self.ksplit, self.strips, self.tiles)
+        return _lib.QmvPlan(_KERNEL_CODES[self.kernel], self.ksplit, self.strips, self.tiles,
+                            self.order)
 
     @classmethod
     def from_c(cls, p) -> "QmvPlan":
-        return cls(_KERNELS[p.kernel], p.ksplit, p.strips, p.tiles)
+        return cls(_KERNELS[p.kernel], p.ksplit, p.strips, p.tiles, p.order)
 
     @property
     def workgroups(self) -> int:

@@ -1,6 +1,7 @@
 """The GEMV plans of the small-row projections (up to 4 rows, no K split) on the GPU.
 
-Every GEMV plan (2 or 4 columns per workgroup, 1 to 8 waves) is installed in turn and run
+Every GEMV plan (2 or 4 columns per workgroup, 1 to 8 waves, both workgroup orders) is
+installed in turn and run
 through the C ABI at 1 to 4 rows, bf16 and f16, 4 and 8 bits, groups of 32 to 128, with and
 without the residual, at K shorter than one pass of the workgroup's lanes and at K that leaves
 a ragged last pass:

@@ -150,8 +150,10 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
     def fits(c, w):
         return chunks <= 64 * w or nproj * c * min(bucket, 4) <= 8
 
-    assert sorted((n // c.strips, c.tiles) for c in gemv) == (
-        sorted((c, w) for c in (2, 4) for w in waves if fits(c, w)) if bucket <= 4 else [])
+    # ... each in both workgroup orders
+    assert sorted((n // c.strips, c.tiles, c.order) for c in gemv) == (
+        sorted((c, w, o) for c in (2, 4) for w in waves for o in (0, 1) if fits(c, w))
+        if bucket <= 4 else [])
     for c in cands:
         assert c.kernel in ("staged", "register", "gemv")
         if c.kernel == "register":
@@ -204,6 +206,8 @@ def test_installed_plans_are_bucketed_per_dtype_and_size_the_workspace(clean_pla
     (QmvPlan("gemv", 1, 1120, 4), "N/2 or N/4"),            # 8 columns per workgroup
     (QmvPlan("gemv", 1, 2240, 0), "in 1..8"),
     (QmvPlan("gemv", 1, 2240, 9), "in 1..8"),
+    (QmvPlan("gemv", 1, 2240, 1, 2), "order must be 0 or 1"),
+    (QmvPlan("staged", 1, 280, 1, 1), "order is a GEMV plan field"),
 ])
 def test_invalid_qmv_plans_are_rejected(plan, message, clean_plans):
     import torch
