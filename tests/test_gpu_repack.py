@@ -11,7 +11,7 @@ import torch
 
 import metile_amd as mt
 from oracle import affine as O
-from tests.helpers import act_to_torch, affine_to_torch, words_to_torch
+from tests.helpers import act_to_torch, affine_to_torch, torch_to_act, words_to_torch
 
 pytestmark = pytest.mark.gpu
 
@@ -112,3 +112,32 @@ def test_executor_on_repacked_weights_equals_the_native_path():
     assert _same(ex1(x[:1], r[:1]), mt.affine_mlp(x[:1], *ts, residual=r[:1]))
     sw = mt.mlx_affine_swiglu_executor(x, *ts[0], *ts[1])
     assert _same(sw(x), mt.affine_swiglu(x, *ts[0], *ts[1]))
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_mlp_mixed_layouts_with_gemv_plans_f16(m):
+    # f16 codes, the down stage on an installed GEMV plan, gate/up on the planner's: every
+    # combination of stage layouts gives the bits of the all-MLX call
+    from metile_amd import tuning
+
+    h, i = 1024, 3072
+    gate = affine_to_torch(O.make_affine_weight(i, h, 4, 64, 8, 10, "f16"), "f16")
+    up = affine_to_torch(O.make_affine_weight(i, h, 4, 64, 8, 12, "f16"), "f16")
+    down = affine_to_torch(O.make_affine_weight(h, i, 4, 64, 8, 14, "f16"), "f16")
+    x = act_to_torch(O.make_activations(m, h, 8, dtype="f16"), "f16")
+    r = act_to_torch(O.make_activations(m, h, 8, tensor_id=3, dtype="f16"), "f16")
+    tuning.clear_plans()
+    try:
+        tuning.install_qmv_plan(m, i, h, 64, 4, 1, torch.float16,
+                                tuning.QmvPlan("gemv", 1, h // 2, 3, 1))
+        want = mt.affine_mlp(x, gate, up, down, residual=r)
+        rp = [(mt.affine_repack(t[0]), t[1], t[2]) for t in (gate, up, down)]
+        for g, u, d in ((rp[0], rp[1], down), (gate, up, rp[2]), tuple(rp)):
+            assert _same(mt.affine_mlp(x, g, u, d, residual=r), want)
+        ref, _ = O.affine_mlp(torch_to_act(x, "f16"), *[
+            (t[0].cpu().numpy().view(np.uint32), torch_to_act(t[1], "f16"),
+             torch_to_act(t[2], "f16")) for t in (gate, up, down)], 64, 4,
+            residual=torch_to_act(r, "f16"), dtype="f16")
+        assert O.tolerance_error(torch_to_act(want, "f16"), ref, "f16") <= 2e-3
+    finally:
+        tuning.clear_plans()
