@@ -7,7 +7,10 @@
 // lanes (1 to 8 waves; the plan picks the fewest that cover K in a given number of passes) split
 // K into 16-byte code chunks (32 codes at 4 bits, 16 at 8 bits): lane t takes the chunks t,
 // t + lanes, t + 2 lanes, ... of every one of the workgroup's columns, and loads the activations
-// of a chunk once for all COLS columns. A chunk's codes are unpacked to exact
+// of a chunk once for all COLS columns. When K is short enough for one pass and a column's
+// chunks fill whole rows of 16 lanes, a workgroup covers several groups of COLS columns, lane t
+// taking chunk t % chunks of group t / chunks (K = 1536 at 4 bits: 48 chunks, three waves serve
+// four groups with no idle lane). A chunk's codes are unpacked to exact
 // 16-bit floats offset + q in K order and dotted with the activations two at a time (fp32
 // accumulate), together with the activations' sum; the group's affine terms are applied in
 // fp32 as in the staged kernel: acc += s * sum_k x_k (offset + q_k) + (b - offset * s) sum_k x_k.
@@ -37,8 +40,19 @@ __device__ __forceinline__ int gemv_column_group(int b, int groups) {
 }
 
 // ONE_PASS: every lane has at most one chunk per column (K / chunk <= lanes), so no second
-// pass is held in registers (more waves fit on a CU).
-template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS>
+// pass is held in registers (more waves fit on a CU). GROUPS: the workgroup covers several
+// column groups (one pass only); a separate instance, so that one-group workgroups keep their
+// columns wave-uniform and issue their loads without the per-lane group arithmetic.
+// `off`, or an offset at or past kOOB (reads zero) when the lane has nothing to load. Written as
+// a bit operation rather than a select: with a select the compiler split the loads into two
+// branch arms writing the same registers, and the second arm then waited for every load in
+// flight (s_waitcnt vmcnt(0)) before issuing, one memory round trip per column. Every buffer
+// here is below 2 GiB, so setting bit 31 is enough.
+__device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) {
+  return off | ((uint32_t)!ok << 31);
+}
+
+template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS, bool GROUPS>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams p) {
   constexpr int kChunks = BITS / 2;        // 16-byte chunks per column and 64-wide K step
   constexpr int kCodes = 128 / BITS;       // codes per chunk
@@ -52,9 +66,17 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   const int wave = tid >> 6;
   const int waves = blockDim.x >> 6;
   const int lanes = blockDim.x;
-  const int col0 = (p.order ? gemv_column_group(blockIdx.x, gridDim.x) : blockIdx.x) * COLS;
   const int M = p.M, K = p.K, N = p.N;
   const int chunks = K / kCodes;
+  // One pass over short K: the workgroup covers `groups` column groups, lane t group t / chunks
+  // and chunk t % chunks (lanes past the last group load nothing). Otherwise one group.
+  static_assert(ONE_PASS || !GROUPS, "column groups need one pass");
+  const int groups = GROUPS ? affine_gemv_groups(K, BITS, waves) : 1;
+  const int gi = GROUPS ? tid / chunks : 0;
+  const int kc0 = GROUPS ? tid % chunks : tid;
+  const bool lane_on = !GROUPS || gi < groups;
+  const int wg = p.order ? gemv_column_group(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int col0 = (wg * groups + gi) * COLS;  // this lane's first column
   const int gshift = __builtin_ctz((unsigned)p.G);
   const int groups_per_row = K >> gshift;
 
@@ -73,7 +95,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
     uint32_t s[NPROJ][COLS], b[NPROJ][COLS];
   };
   auto load = [&](Stage& S, int kc) {
-    const bool ok = kc < chunks;
+    const bool ok = lane_on && kc < chunks;
     const int st = kc / kChunks;
     const uint32_t wo = (uint32_t)st * p.step_stride + 16u * (uint32_t)(kc % kChunks);
     const int k0 = kc * kCodes;
@@ -82,9 +104,9 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 #pragma unroll
       for (int j = 0; j < COLS; ++j) {
         const uint32_t col = (uint32_t)(col0 + j);
-        S.q[pr][j] = load16(rw[pr], ok ? col * p.col_stride + wo : kOOB);
+        S.q[pr][j] = load16(rw[pr], oob_unless(ok, col * p.col_stride + wo));
         const uint32_t go =
-            ok ? (col * (uint32_t)groups_per_row + (uint32_t)(k0 >> gshift)) * 2u : kOOB;
+            oob_unless(ok, (col * (uint32_t)groups_per_row + (uint32_t)(k0 >> gshift)) * 2u);
         S.s[pr][j] = load2(rs[pr], go);
         S.b[pr][j] = load2(rb[pr], go);
       }
@@ -92,7 +114,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
     for (int m = 0; m < ROWS; ++m)
 #pragma unroll
       for (int v = 0; v < kXLoads; ++v)
-        S.x[m][v] = load16(rx, (ok && m < M) ? ((uint32_t)m * K + k0 + 8 * v) * 2u : kOOB);
+        S.x[m][v] = load16(rx, oob_unless(ok && m < M, ((uint32_t)m * K + k0 + 8 * v) * 2u));
   };
 
   float acc[NPROJ][COLS][ROWS];
@@ -151,7 +173,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   // count is the same for every lane (lanes past K load zeros), so the branches are uniform.
   if constexpr (ONE_PASS) {
     Stage cur;
-    load(cur, tid);
+    load(cur, kc0);
     compute(cur);
   } else {
     Stage cur, nxt;
@@ -164,7 +186,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
     }
   }
 
-  // Rows of 16 lanes by DPP (each lane ends with its row's sum), then rows and waves in LDS.
+  // Rows of 16 lanes by DPP (each lane ends with its row's sum; a row never spans two groups),
+  // then a group's rows in LDS, in row order.
 #pragma unroll
   for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
@@ -176,19 +199,19 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
         if ((lane & 15) == 0) red[wave][(pr * COLS + j) * ROWS + m][lane >> 4] = v;
       }
   __syncthreads();
-  if (tid < COLS * ROWS) {
-    const int j = tid / ROWS, m = tid % ROWS;
+  if (tid < groups * COLS * ROWS) {
+    const int g = tid / (COLS * ROWS), j = (tid / ROWS) % COLS, m = tid % ROWS;
+    const int r0 = GROUPS ? g * (chunks / 16) : 0;
+    const int r1 = GROUPS ? r0 + chunks / 16 : 4 * waves;
     float v[NPROJ];
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr) {
       float s = 0.0f;
-      for (int w = 0; w < waves; ++w)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s += red[w][(pr * COLS + j) * ROWS + m][r];
+      for (int r = r0; r < r1; ++r) s += red[r >> 2][(pr * COLS + j) * ROWS + m][r & 3];
       v[pr] = s;
     }
     if (m < M) {
-      const size_t o = (size_t)m * N + col0 + j;
+      const size_t o = (size_t)m * N + (wg * groups + g) * COLS + j;
       float out;
       if constexpr (NPROJ == 2) {
         out = silu_mul(v[0], v[1]);
@@ -204,11 +227,18 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
 hipError_t launch_waves(const QmvParams& p, int waves, hipStream_t stream) {
   if (affine_gemv_one_pass(p.K, BITS, waves)) {
-    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
+    const int groups = affine_gemv_groups(p.K, BITS, waves);
+    if (groups > 1)
+      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, true>
+          <<<p.N / (COLS * groups), 64 * waves, 0, stream>>>(p);
+    else
+      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, false>
+          <<<p.N / COLS, 64 * waves, 0, stream>>>(p);
     return hipGetLastError();
   }
   if constexpr (affine_gemv_fits(ROWS, NPROJ, COLS, false)) {
-    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false><<<p.N / COLS, 64 * waves, 0, stream>>>(p);
+    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false, false>
+        <<<p.N / COLS, 64 * waves, 0, stream>>>(p);
     return hipGetLastError();
   }
   return hipErrorInvalidValue;
@@ -240,7 +270,8 @@ hipError_t launch_bits_dt(const QmvParams& p, int nproj, int waves, int cols,
 
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream) {
-  if (p.N % cols || p.K % 64 || p.G < 32 || waves < 1 || waves > kGemvMaxWaves ||
+  if (p.K % 64 || p.G < 32 || waves < 1 || waves > kGemvMaxWaves ||
+      p.N % (cols * affine_gemv_groups(p.K, bits, waves)) ||
       !affine_gemv_fits(p.M, nproj, cols, affine_gemv_one_pass(p.K, bits, waves)))
     return hipErrorInvalidValue;
   if (bits == 4) {

@@ -122,6 +122,15 @@ __host__ __device__ constexpr bool affine_gemv_fits(int rows, int nproj, int col
 __host__ __device__ constexpr bool affine_gemv_one_pass(int K, int bits, int waves) {
   return K * bits / 128 <= 64 * waves;
 }
+// Column groups (of `cols` columns each) one workgroup covers: in one pass, when a column's
+// chunks fill whole rows of 16 lanes (so DPP row sums never mix groups), as many groups as its
+// lanes hold (lane t: group t / chunks, chunk t % chunks); otherwise one. Grid: N / (cols *
+// groups) workgroups.
+__host__ __device__ constexpr int affine_gemv_groups(int K, int bits, int waves) {
+  return affine_gemv_one_pass(K, bits, waves) && (K * bits / 128) % 16 == 0
+             ? 64 * waves / (K * bits / 128)
+             : 1;
+}
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream);
 

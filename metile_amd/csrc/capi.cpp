@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -299,12 +300,14 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
   if (q.kernel == MT_QMV_GEMV) {
     if (rows > mt::kGemvMaxRows) return "more rows than the GEMV kernel takes";
     if (q.ksplit != 1) return "the GEMV kernel does not split K";
-    if (q.strips < 1 || N % q.strips || (N / q.strips != 2 && N / q.strips != 4))
-      return "GEMV strips must be N/2 or N/4";
     if (q.tiles < 1 || q.tiles > mt::kGemvMaxWaves)
       return "GEMV tiles (waves per workgroup) must be in 1..8";
+    const int groups = mt::affine_gemv_groups(K, bits, q.tiles);
+    if (q.strips < 1 || N % (q.strips * groups) ||
+        (N / q.strips / groups != 2 && N / q.strips / groups != 4))
+      return "GEMV strips must be N/(2 groups) or N/(4 groups)";
     if (q.order != 0 && q.order != 1) return "GEMV order must be 0 or 1";
-    if (!mt::affine_gemv_fits(rows, nproj, N / q.strips,
+    if (!mt::affine_gemv_fits(rows, nproj, N / q.strips / groups,
                               mt::affine_gemv_one_pass(K, bits, q.tiles)))
       return "the GEMV kernel does not hold this many columns and rows in registers";
     return "";
@@ -375,7 +378,8 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
       }
   }
   // GEMV: for each number of passes over K (one 16-byte chunk of codes per lane and pass), the
-  // fewest waves that make it.
+  // fewest waves that make it; in one pass, also the wave counts whose lanes hold two or more
+  // whole column groups with no lane idle.
   const int chunks = K * bits / 128;
   std::vector<int> waves;
   for (int passes = 1; passes <= 2 * mt::kGemvMaxWaves; ++passes) {
@@ -383,10 +387,16 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
     if (w <= mt::kGemvMaxWaves && (waves.empty() || waves.back() != w)) waves.push_back(w);
     if (w == 1) break;
   }
+  for (int w = 1; w <= mt::kGemvMaxWaves; ++w)
+    if (mt::affine_gemv_groups(K, bits, w) >= 2 && (64 * w) % chunks == 0 &&
+        std::find(waves.begin(), waves.end(), w) == waves.end())
+      waves.push_back(w);
   for (int cols : {4, 2})
     for (int w : waves)
       for (int order : {1, 0}) {
-        const mt_qmv_plan g{MT_QMV_GEMV, 1, N / cols, w, order};
+        const int per_wg = cols * mt::affine_gemv_groups(K, bits, w);
+        if (N % per_wg) continue;
+        const mt_qmv_plan g{MT_QMV_GEMV, 1, N / per_wg, w, order};
         if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
       }
   return out;
@@ -505,7 +515,9 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     set_layout(p, layout, bits);
     hipError_t e;
     if (plan.kernel == MT_QMV_GEMV)
-      e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles, N / plan.strips, hs);
+      e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles,
+                                 N / plan.strips / mt::affine_gemv_groups(K, bits, plan.tiles),
+                                 hs);
     else if (plan.kernel == MT_QMV_STAGED)
       e = mt::launch_affine_qmv_lds(p, bits, dtype, nproj, hs);
     else

@@ -88,17 +88,24 @@ def test_gemv_plans_match_the_oracle_at_every_row_count(case):
         r = None if rt is None else rt[:rows]
         return mt.affine_qmv(xt[:rows], *ts[0], group_size=g, bits=bits, residual=r)
 
+    chunks = k * bits // 128
+
+    def groups(w):  # column groups per workgroup (one pass over K in whole rows of 16 lanes)
+        return 64 * w // chunks if chunks <= 64 * w and chunks % 16 == 0 else 1
+
     plans = [p for p in tuning.qmv_plan_candidates(1, k, n, g, bits, nproj) if p.kernel == "gemv"]
     # the listed wave counts, and the extremes (one wave: many passes; eight: lanes to spare)
-    plans += [tuning.QmvPlan("gemv", 1, n // c, w) for c in (2, 4) for w in (1, 8)]
+    plans += [tuning.QmvPlan("gemv", 1, n // (c * groups(w)), w) for c in (2, 4) for w in (1, 8)
+              if n % (c * groups(w)) == 0]
     plans = list(dict.fromkeys(plans))
     worst = 0.0
     for plan in plans:
         outs = {}
         for rows in (1, 2, 3, 4):
             print(f"[{case}] plan {plan} rows {rows}", flush=True)
-            one_pass = k * bits // 128 <= 64 * plan.tiles
-            if not one_pass and nproj * (n // plan.strips) * (4 if rows > 2 else rows) > 8:
+            one_pass = chunks <= 64 * plan.tiles
+            cols = n // plan.strips // groups(plan.tiles)
+            if not one_pass and nproj * cols * (4 if rows > 2 else rows) > 8:
                 continue  # two passes of this many columns and rows would spill registers
             tuning.install_qmv_plan(rows, k, n, g, bits, nproj, tdt, plan)
             a, b = run(mlx, rows), run(packed, rows)
