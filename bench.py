@@ -196,10 +196,13 @@ def kernel_label(k, n, nproj):
 
     plan = tuning.qmv_plan(1, k, n, GROUP, BITS, nproj, torch.bfloat16)
     if plan.kernel == "gemv":
-        cols, waves = n // plan.strips, plan.tiles
-        one_pass = "true" if k * BITS // 128 <= 64 * waves else "false"
-        return (f"affine_gemv_kernel<{BITS}, 0, 1, {nproj}, {cols}, {one_pass}> "
-                f"({plan.strips} workgroups of {waves} waves)")
+        waves, chunks = plan.tiles, k * BITS // 128
+        one_pass = chunks <= 64 * waves
+        groups = 64 * waves // chunks if one_pass and chunks % 16 == 0 else 1
+        cols = n // plan.strips // groups
+        flags = f"{str(one_pass).lower()}, {str(groups > 1).lower()}"
+        return (f"affine_gemv_kernel<{BITS}, 0, 1, {nproj}, {cols}, {flags}> "
+                f"({plan.strips} workgroups of {waves} waves, {groups} column groups each)")
     if plan.kernel == "staged":
         return (f"affine_qmv_lds_kernel<{BITS}, 0, 8, {nproj}, ...> "
                 f"({plan.strips} strips, {plan.ksplit} K splits)")
