@@ -128,8 +128,9 @@ def test_mlp_mixed_layouts_with_gemv_plans_f16(m):
     r = act_to_torch(O.make_activations(m, h, 8, tensor_id=3, dtype="f16"), "f16")
     tuning.clear_plans()
     try:
+        # K = 3072 is 96 chunks: three waves cover two groups of two columns (N / 4 workgroups)
         tuning.install_qmv_plan(m, i, h, 64, 4, 1, torch.float16,
-                                tuning.QmvPlan("gemv", 1, h // 2, 3, 1))
+                                tuning.QmvPlan("gemv", 1, h // 4, 3, 1))
         want = mt.affine_mlp(x, gate, up, down, residual=r)
         rp = [(mt.affine_repack(t[0]), t[1], t[2]) for t in (gate, up, down)]
         for g, u, d in ((rp[0], rp[1], down), (gate, up, rp[2]), tuple(rp)):
