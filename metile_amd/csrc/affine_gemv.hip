@@ -43,15 +43,6 @@ __device__ __forceinline__ int gemv_column_group(int b, int groups) {
 // pass is held in registers (more waves fit on a CU). GROUPS: the workgroup covers several
 // column groups (one pass only); a separate instance, so that one-group workgroups keep their
 // columns wave-uniform and issue their loads without the per-lane group arithmetic.
-// `off`, or an offset at or past kOOB (reads zero) when the lane has nothing to load. Written as
-// a bit operation rather than a select: with a select the compiler split the loads into two
-// branch arms writing the same registers, and the second arm then waited for every load in
-// flight (s_waitcnt vmcnt(0)) before issuing, one memory round trip per column. Every buffer
-// here is below 2 GiB, so setting bit 31 is enough.
-__device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) {
-  return off | ((uint32_t)!ok << 31);
-}
-
 template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS, bool GROUPS>
 __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams p) {
   constexpr int kChunks = BITS / 2;        // 16-byte chunks per column and 64-wide K step

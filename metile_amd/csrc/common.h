@@ -28,6 +28,14 @@ enum Dtype : int { kBF16 = 0, kF16 = 1 };
 // Offsets at or above every buffer size used here read as zero.
 constexpr uint32_t kOOB = 0x80000000u;
 
+// `off`, or an offset at or past kOOB (reads zero) when the lane has nothing to load. Written as
+// a bit operation rather than a select: with a select the compiler split loads into two branch
+// arms writing the same registers, and the second arm then waited for every load in flight
+// (s_waitcnt vmcnt(0)) before issuing. Every buffer here is below 2 GiB, so bit 31 suffices.
+__device__ __forceinline__ uint32_t oob_unless(bool ok, uint32_t off) {
+  return off | ((uint32_t)!ok << 31);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   // Word 3 = 0x00020000: raw (unswizzled, untyped) dword access on gfx9-family parts.
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
