@@ -490,7 +490,7 @@ def tuning_report(args):
         return ",".join(f"{k}={v}" for k, v in plan.items())
 
     decisions = []
-    for e in tuning.read_json(tuning.cache_path(), {}).values():
+    for e in tuning.cached_decisions():
         decisions.append({
             "op": e.get("op"), "rows": e.get("rows"), "K": e.get("input_features"),
             "N": e.get("output_features"), "bits": e.get("bits"), "nproj": e.get("nproj", 1),

@@ -134,22 +134,6 @@ __host__ __device__ constexpr int affine_gemv_groups(int K, int bits, int waves)
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream);
 
-// One-launch quantized MLP, y = down(silu(gate x) * up x) (+ residual), for M <= 16.
-// Workgroups [0, blocks_up) compute the gate/up strips of `up` (its y is the hidden
-// activation h in the workspace) and publish each finished hidden strip; the remaining
-// workgroups compute the down strips of `down` (x = h) and start their K range once every
-// hidden strip in it is published. Workgroups are dispatched in index order, so every
-// gate/up workgroup has started before any down workgroup waits; the waits are bounded.
-struct MlpLink {
-  uint32_t* ready;  // [down splits] hidden strips published in each down split's K range
-  uint32_t* done;   // down workgroups finished; the last one clears ready[] and done
-  int hstrips_per_split;
-  int down_blocks;
-  int prefetch_at;  // published strips of its split before a down workgroup requests codes
-};
-
-hipError_t launch_affine_mlp_fused(const QmvParams& up, const QmvParams& down,
-                                   const MlpLink& link, int bits, int dtype, hipStream_t stream);
 
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                                     float* out, int N, int K, int G, int bits, int dtype,

@@ -1,10 +1,8 @@
-// Activation-staged small-row affine projections (M <= 16) and the one-launch quantized MLP,
-// for gfx950.
+// Activation-staged small-row affine projections (M <= 16) for gfx950.
 //
 // Same contract as affine_qmv.hip: y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/G] + b[n, k/G])
 // (reference semantics kernels/affine_qmv.py:4-54; residual and SwiGLU epilogues
-// kernels/affine_qmv.py:124-132,204-214; the MLP composition of mlx_affine_mlp_executor,
-// metile/backends/mlx_quantized.py:1770-1832), with the same work split (32-column strips x
+// kernels/affine_qmv.py:124-132,204-214), with the same work split (32-column strips x
 // K splits, four to eight K steps per wave), scale staging, fixed-order cross-wave reduction and
 // deterministic split-K protocol. What differs from affine_qmv_kernel:
 //  * The workgroup's activation rows for its K range are loaded once and parked in LDS. For
@@ -16,34 +14,14 @@
 //    their sums with three lane exchanges.
 //  * The register ring holds codes only, so a wave needs about half the registers and a
 //    workgroup runs eight waves.
-//
-// The one-launch MLP runs the gate/up strips and the down strips as two sets of workgroups of
-// one grid. A gate/up workgroup that finishes a hidden strip (32 columns of
-// h = silu(gate x) * up x, rounded to the activation type) writes it with device-coherent
-// stores and counts it into ready[] of the down K split that reads it. A down workgroup issues
-// its scale and code loads first, then waits until its K split's hidden strips are all counted,
-// then reads h with device-coherent loads. The last down workgroup to finish clears the
-// hand-off counters, so every call starts from zero. This removes the second launch's fixed
-// latency and lets the down weights stream while the gate/up strips are still computing.
 #include "common.h"
 #include "affine_qmv.h"
 
 namespace mt {
 namespace {
 
-enum Role : int { kPlain = 0, kGateUp = 1, kDown = 2 };
-
 // Code stages each wave requests before the workgroup parks its scales and activations.
 constexpr int kQmvEarlyStages = 2;
-
-// Polls of the hand-off counter before a down workgroup gives up (about 60 ms); its outputs
-// are then NaN, so a broken hand-off is loud and the grid still drains.
-constexpr uint32_t kSpinLimit = 1u << 20;
-
-template <int DT>
-__device__ __forceinline__ uint16_t quiet_nan() {
-  return DT == kBF16 ? (uint16_t)0x7FC0u : (uint16_t)0x7E00u;
-}
 
 // One workgroup's share: TILES consecutive output strips (strip s = columns [s N / strips,
 // (s + 1) N / strips), at most 32), strips [group TILES, group TILES + TILES), over K split
@@ -53,12 +31,9 @@ __device__ __forceinline__ uint16_t quiet_nan() {
 // HALF: groups of 32, two per 64-wide K step. Each projection then runs two MFMA chains per
 // step, one per group: lanes of the other K half (h) read the zero row, so each chain sums one
 // group only and gets its own scale, bias and row sum.
-template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, int ROLE, bool HALF,
-          int TILES>
+template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, int EARLY, bool HALF, int TILES>
 __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, const int split,
-                                         unsigned char* __restrict__ dyn, int* flag,
-                                         const MlpLink& link) {
-  static_assert(ROLE == kPlain || TILES == 1, "the one-launch MLP uses one strip per workgroup");
+                                         unsigned char* __restrict__ dyn, int* flag) {
   constexpr int WAVES = kQmvLdsWaves;  // per tile
   constexpr int kTileThreads = WAVES * 64;
   constexpr int kThreads = kTileThreads * TILES;
@@ -150,10 +125,10 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
       const int cc = c - row * cpr;
       const uint32_t off =
           c < nchunks ? ((uint32_t)row * K + (uint32_t)(s_beg * 64 + cc * 8)) * 2u : kOOB;
-      xv[i] = ROLE == kDown ? load16_device(rx, off) : load16(rx, off);
+      xv[i] = load16(rx, off);
     }
   };
-  if constexpr (ROLE != kDown) issue_x();
+  issue_x();
 
   // ---- code ring ---------------------------------------------------------------------------
   const uint32_t w_row =
@@ -168,37 +143,12 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
 #pragma unroll
       for (int v = 0; v < BITS / 4; ++v) S[pr][v] = load16(rw[pr], ok ? woff + 16u * v : kOOB);
   };
-  // ---- down workgroups: wait until the hidden strips of this K split are published --------
-  // The codes are requested once link.prefetch_at strips of the split are published (0: at
-  // once), the hidden activation once all are.
-  bool timed_out = false;
-  auto wait_ready = [&](uint32_t target) {
-    if (tid == 0) {
-      uint32_t spins = 0;
-      while (__hip_atomic_load(&link.ready[split], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) <
-             target) {
-        __builtin_amdgcn_s_sleep(2);
-        if (++spins == kSpinLimit) break;
-      }
-      flag[0] = spins == kSpinLimit;
-    }
-    __syncthreads();
-    return flag[0] != 0;
-  };
-  const uint32_t need = (uint32_t)(2 * steps_here);
-  if constexpr (ROLE == kDown) {
-    if (link.prefetch_at > 0) timed_out = wait_ready(min((uint32_t)link.prefetch_at, need));
-  }
   // The first EARLY stages are requested before the scales and activations are parked, the
   // rest after: requests behind the bulk of the grid's code stream would otherwise hold up
   // the data every K step depends on.
-  constexpr int kEarly = (ROLE == kDown || EARLY > STAGES) ? STAGES : EARLY;
+  constexpr int kEarly = EARLY > STAGES ? STAGES : EARLY;
 #pragma unroll
   for (int d = 0; d < kEarly; ++d) load_stage(ring[d], w_beg + d);
-  if constexpr (ROLE == kDown) {
-    if (!timed_out) timed_out = wait_ready(need);
-    issue_x();
-  }
 
   // ---- park scales, biases and activations in LDS; per-step row sums ----------------------
 #pragma unroll
@@ -329,7 +279,6 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
     return v;
   };
 
-  const __amdgpu_buffer_rsrc_t ry = make_rsrc(p.y, (uint32_t)M * N * 2u);
   // Final value of output (i, c) of this strip from its K sums v[].
   auto finish = [&](int i, int c, const float (&v)[NPROJ]) {
     const size_t oi = (size_t)i * N + col0 + c;
@@ -340,37 +289,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
       out = v[0];
       if (p.residual) out += act_to_f32<DT>(res_pre);  // output i * 32 + c is this thread's
     }
-    const uint16_t o16 = timed_out ? quiet_nan<DT>() : f32_to_act<DT>(out);
-    if constexpr (ROLE == kGateUp) {
-      store2_device(ry, (uint32_t)oi * 2u, o16);
-    } else {
-      p.y[oi] = o16;
-    }
-  };
-  // Gate/up: after this workgroup's stores of a finished hidden strip have completed, count
-  // the strip into its down split.
-  auto publish = [&]() {
-    if constexpr (ROLE == kGateUp) {
-      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      if (tid == 0)
-        __hip_atomic_fetch_add(&link.ready[strip / link.hstrips_per_split], 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
-  // Down: count this workgroup out; the last one clears the hand-off counters.
-  auto retire = [&]() {
-    if constexpr (ROLE == kDown) {
-      if (tid == 0) {
-        const unsigned prev =
-            __hip_atomic_fetch_add(link.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev == (unsigned)(link.down_blocks - 1)) {
-          for (int b = 0; b < p.ksplit; ++b)
-            __hip_atomic_store(&link.ready[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(link.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
+    p.y[oi] = f32_to_act<DT>(out);
   };
 
   const int outs = M * 32;
@@ -382,8 +301,6 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
       for (int pr = 0; pr < NPROJ; ++pr) v[pr] = reduce(pr, o >> 5, o & 31);
       finish(o >> 5, o & 31, v);
     }
-    publish();
-    retire();
     return;
   }
 
@@ -411,10 +328,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   }
   __syncthreads();
   // No workgroup barrier follows: one tile may return while the other finishes its strip.
-  if (!flag[tile]) {
-    retire();
-    return;
-  }
+  if (!flag[tile]) return;
   for (int o = ttid; o < outs; o += kTileThreads) {
     const int i = o >> 5, c = o & 31;
     if (c >= width) continue;
@@ -428,8 +342,6 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   }
   if (ttid == 0)
     __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  publish();
-  retire();
 }
 
 // At most 128 registers, so that sixteen waves (two one-tile workgroups or one two-tile
@@ -439,30 +351,9 @@ __global__ __launch_bounds__(kQmvLdsWaves * 64 * TILES) __attribute__((amdgpu_wa
 void affine_qmv_lds_kernel(const QmvParams p) {
   extern __shared__ __align__(16) unsigned char dyn_plain[];
   __shared__ int flag[TILES];
-  const MlpLink none{};
-  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, kPlain, HALF, TILES>(
-      p, blockIdx.x, blockIdx.y, dyn_plain, flag, none);
-}
-
-template <int BITS, int DT, int MROWS>
-__global__ __launch_bounds__(kQmvLdsWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
-void affine_mlp_kernel(const QmvParams up, const QmvParams down, const MlpLink link,
-                       int blocks_up) {
-  extern __shared__ __align__(16) unsigned char dyn_mlp[];
-  __shared__ int flag;
-  constexpr int kStagesUp = BITS == 4 ? 4 : 2;
-  constexpr int kStagesDown = BITS == 4 ? 6 : 4;
-  const int id = blockIdx.x;
-  if (id < blocks_up) {
-    const int strips = up.strips;
-    lds_task<BITS, DT, MROWS, 2, kStagesUp, kQmvEarlyStages, kGateUp, false, 1>(
-        up, id % strips, id / strips, dyn_mlp, &flag, link);
-  } else {
-    const int strips = down.strips;
-    const int idd = id - blocks_up;
-    lds_task<BITS, DT, MROWS, 1, kStagesDown, kStagesDown, kDown, false, 1>(
-        down, idd % strips, idd / strips, dyn_mlp, &flag, link);
-  }
+  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, HALF, TILES>(p, blockIdx.x,
+                                                                         blockIdx.y, dyn_plain,
+                                                                         flag);
 }
 
 // Raises a kernel's dynamic LDS limit (64 KiB by default) to what a workgroup of `tiles`
@@ -527,28 +418,6 @@ hipError_t launch_lds_bits_dt(const QmvParams& p, int nproj, hipStream_t stream)
                     : launch_lds_nproj<BITS, DT, 1>(p, stream);
 }
 
-template <int BITS, int DT, int MROWS>
-hipError_t launch_mlp_rows(const QmvParams& up, const QmvParams& down, const MlpLink& link,
-                           hipStream_t stream) {
-  const QmvLdsLayout la = qmv_lds_layout(up.M, up.steps_per_split, MROWS, 2, 1, 1);
-  const QmvLdsLayout lb = qmv_lds_layout(down.M, down.steps_per_split, MROWS, 1, 1, 1);
-  const int blocks_up = up.strips * up.ksplit;
-  const int blocks = blocks_up + link.down_blocks;
-  auto kernel = affine_mlp_kernel<BITS, DT, MROWS>;
-  static const hipError_t attr = allow_lds(reinterpret_cast<const void*>(kernel), 1);
-  if (attr != hipSuccess) return attr;
-  kernel<<<dim3(blocks), dim3(kQmvLdsWaves * 64), la.bytes > lb.bytes ? la.bytes : lb.bytes,
-           stream>>>(up, down, link, blocks_up);
-  return hipGetLastError();
-}
-
-template <int BITS, int DT>
-hipError_t launch_mlp_bits_dt(const QmvParams& up, const QmvParams& down, const MlpLink& link,
-                              hipStream_t stream) {
-  return up.M <= 8 ? launch_mlp_rows<BITS, DT, 8>(up, down, link, stream)
-                   : launch_mlp_rows<BITS, DT, 16>(up, down, link, stream);
-}
-
 }  // namespace
 
 bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size, int tiles) {
@@ -572,16 +441,6 @@ hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int np
   }
   return dtype == kBF16 ? launch_lds_bits_dt<8, kBF16>(p, nproj, stream)
                         : launch_lds_bits_dt<8, kF16>(p, nproj, stream);
-}
-
-hipError_t launch_affine_mlp_fused(const QmvParams& up, const QmvParams& down,
-                                   const MlpLink& link, int bits, int dtype, hipStream_t stream) {
-  if (bits == 4) {
-    return dtype == kBF16 ? launch_mlp_bits_dt<4, kBF16>(up, down, link, stream)
-                          : launch_mlp_bits_dt<4, kF16>(up, down, link, stream);
-  }
-  return dtype == kBF16 ? launch_mlp_bits_dt<8, kBF16>(up, down, link, stream)
-                        : launch_mlp_bits_dt<8, kF16>(up, down, link, stream);
 }
 
 }  // namespace mt

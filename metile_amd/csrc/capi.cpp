@@ -65,10 +65,6 @@ Plan plan_split(int K, int N) {
   // Each split covers at most kMaxGroupsPerSplit - 1 groups of 64 (one more may straddle).
   const int min_split = (steps + mt::kMaxGroupsPerSplit - 2) / (mt::kMaxGroupsPerSplit - 1);
   if (ksplit < min_split) ksplit = min_split;
-  if (const char* env = std::getenv("METILE_AMD_KSPLIT")) {
-    const int forced = std::atoi(env);
-    if (forced >= min_split && forced <= steps) ksplit = forced;
-  }
   if (ksplit < 1) ksplit = 1;
   Plan p;
   p.steps_per_split = (steps + ksplit - 1) / ksplit;
@@ -80,16 +76,26 @@ Plan plan_split(int K, int N) {
   return p;
 }
 
-// Activation-staged small-row kernel where it fits (M <= 16 and a bounded K range per
-// split); METILE_AMD_QMV_PATH=reg forces the register-staged kernel (for comparisons) except
-// for groups of 32, which only the staged kernel handles.
+// Activation-staged small-row kernel where it fits (M <= 16 and a bounded K range per split).
 bool use_lds_path(int rows, int steps_per_split, int nproj, int group_size) {
-  const char* env = std::getenv("METILE_AMD_QMV_PATH");
-  if (group_size != 32 && env && std::string(env) == "reg") return false;
   return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size, 1);
 }
 
-constexpr int kCus = 256;  // compute units of an MI355X
+// Compute units of the current device (hipDeviceProp_t::multiProcessorCount; 256 on an
+// MI355X), read once per device. Plans depend on it through the workgroups per CU.
+int device_cus() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus > 0) return cus;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  cached[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
 
 // Largest K split the tuner's candidate lists go to.
 constexpr int kMaxCandidateSplits = 32;
@@ -115,7 +121,7 @@ int staged_ring(int bits, int nproj, int group_size) {
 // 5.16 us, 152 strips 4.99 us). Only grids that are resident at once (two eight-wave
 // workgroups per CU) are rebalanced: a grid of several rounds evens out as workgroups
 // retire. (Changing the K split instead also measured slower: every split adds a partial-sum
-// hand-off.) METILE_AMD_STRIPS=32 keeps 32-column strips.
+// hand-off.)
 Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   Plan plan = plan_split(K, N);
   if (group_size == 32) {
@@ -139,8 +145,9 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   // grids of
   // several rounds of workgroups anyway, until every wave's K steps fit its code ring (a ring
   // that refills costs more than the extra split: K = 5120, N = 17408 at 8 bits measured
-  // 30.3 us with 3 splits against 32.7 us with 2). A forced METILE_AMD_KSPLIT is kept.
-  if (!std::getenv("METILE_AMD_KSPLIT") && group_size != 32) {
+  // 30.3 us with 3 splits against 32.7 us with 2).
+  const int kCus = device_cus();
+  if (group_size != 32) {
     const int steps = K / 64;
     auto split_into = [&](int ks) {
       Plan c = plan;
@@ -169,8 +176,6 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   }
   if (!use_lds_path(rows, plan.steps_per_split, nproj, group_size)) return plan;
   plan.kernel = MT_QMV_STAGED;
-  const char* env = std::getenv("METILE_AMD_STRIPS");
-  if (env && std::string(env) == "32") return plan;
   const long base = N / 32, ks = plan.ksplit;
   const long per_cu_base = (base * ks + kCus - 1) / kCus;  // workgroups on the busiest CU
   const bool rebalance = nproj == 2 && rows <= 2 && base * ks > kCus;
@@ -190,14 +195,9 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   // rows or more: the two strips then share one staging of the activations (half the
   // activation reads through each CU's memory pipeline; SwiGLU 1536 -> 8960 at M = 8: 8.06 us
   // against 8.45 us). At fewer rows that staging is small and the 16-wave workgroup measured
-  // slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us). METILE_AMD_TILES=1 or 2 overrides
-  // where the shape allows.
+  // slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us).
   const long wgs = (long)plan.strips * plan.ksplit;
   int tiles = (rows >= 4 && plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
-  if (const char* t = std::getenv("METILE_AMD_TILES")) {
-    const int forced = std::atoi(t);
-    if (forced == 1 || (forced == 2 && plan.strips % 2 == 0)) tiles = forced;
-  }
   if (tiles == 2 && !mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 2))
     tiles = 1;
   plan.tiles = tiles;
@@ -348,6 +348,7 @@ Plan plan_qmv(int rows, int K, int N, int nproj, int group_size, int bits, int d
 // number of workgroups on every CU within one round above the busiest CU's share.
 std::vector<int> strip_options(int N, int ksplit) {
   std::vector<int> out{N / 32};
+  const int kCus = device_cus();
   const long base = N / 32, per_cu = (base * ksplit + kCus - 1) / kCus;
   for (long rounds = per_cu; rounds <= per_cu + 1; ++rounds) {
     if ((rounds * kCus) % ksplit) continue;
@@ -601,7 +602,6 @@ GemmPlan planner_gemm(int M, int K, int N) {
   const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
   const int t64 = ((M + 63) / 64) * ((N + 63) / 64);
   g.tile = t128 >= 200 ? 2 : 1;
-  if (const char* env = std::getenv("METILE_AMD_GEMM_TILE")) g.tile = std::atoi(env) == 2 ? 2 : 1;
   g.tiles = g.tile == 2 ? t128 : t64;
   // About three workgroups per CU in total, keeping at least 24 K steps per split (measured
   // on MI355X at Qwen2.5-1.5B prefill shapes: up 1536x8960 best unsplit, down 8960x1536 best
@@ -611,10 +611,6 @@ GemmPlan planner_gemm(int M, int K, int N) {
   const int max_split = steps / 24 > 0 ? steps / 24 : 1;
   if (ksplit > max_split) ksplit = max_split;
   if (ksplit < 1) ksplit = 1;
-  if (const char* env = std::getenv("METILE_AMD_GEMM_KSPLIT")) {
-    const int f = std::atoi(env);
-    if (f >= 1 && f <= steps) ksplit = f;
-  }
   g.steps_per_split = (steps + ksplit - 1) / ksplit;
   g.ksplit = (steps + g.steps_per_split - 1) / g.steps_per_split;
   return g;
@@ -698,59 +694,20 @@ size_t gemm_workspace(int M, int K, int N, int group_size) {
   return need;
 }
 
-// ---- one-launch MLP plan ---------------------------------------------------------------
-// Gate/up keeps the small-row plan; the down projection takes as many K splits as fit beside
-// the gate/up workgroups in one resident wave of the grid (two eight-wave workgroups per CU on
-// a 256-CU part), at least what its staging limits require. Depends only on (M, H, I) and the
-// environment override, so the workspace query and the call agree.
-constexpr int kResidentWorkgroups = 512;
-
+// ---- MLP workspace ------------------------------------------------------------------------
+// [counters + split-K partials of either projection | hidden activation]: the gate/up and down
+// launches share the counter region (each leaves it zeroed) and the partial space, which lies
+// below the hidden activation.
 struct MlpPlan {
-  bool fused;
-  Plan up, down;
-  size_t up_partial, down_partial, hidden, bytes;  // workspace offsets (bytes) and total
+  size_t hidden, bytes;  // workspace offset of the hidden activation, and the total
 };
 
 MlpPlan plan_mlp(int M, int H, int I, int group_size, int bits) {
+  const size_t a = qmv_workspace(M, H, I, 2, group_size, bits);
+  const size_t b = qmv_workspace(M, I, H, 1, group_size, bits);
+  const size_t split = align_up(a > b ? a : b);
   MlpPlan mp{};
-  mp.up = plan_split(H, I);
-  mp.down = plan_split(I, H);
-  // The one-launch MLP is opt-in (METILE_AMD_MLP_PATH=fused): on MI355X its hand-off chain
-  // (hidden-strip store acknowledgement, counter, coherent reload) costs several HBM round
-  // trips while the weight stream is still in flight, which measured slower than two launches.
-  const char* env = std::getenv("METILE_AMD_MLP_PATH");
-  const bool forced_split = !(env && std::string(env) == "fused");
-  const int strips_up = I / 32, strips_down = H / 32, steps_down = I / 64;
-  const int blocks_up = strips_up * mp.up.ksplit;
-  int ks = (kResidentWorkgroups - blocks_up) / strips_down;
-  if (ks > mp.down.ksplit) ks = mp.down.ksplit;
-  const int min_split = (steps_down + mt::kMaxGroupsPerSplit - 2) / (mt::kMaxGroupsPerSplit - 1);
-  if (ks < min_split) ks = min_split;
-  if (ks < 1) ks = 1;
-  Plan down{};
-  for (; ks <= steps_down; ++ks) {
-    down.steps_per_split = (steps_down + ks - 1) / ks;
-    down.ksplit = (steps_down + down.steps_per_split - 1) / down.steps_per_split;
-    if (mt::affine_qmv_lds_fits(M, down.steps_per_split, 1, 64, 1)) break;
-  }
-  mp.fused = !forced_split && M <= mt::kQmvLdsMaxRows && ks <= steps_down &&
-             mt::affine_qmv_lds_fits(M, mp.up.steps_per_split, 2, 64, 1) && group_size >= 64 &&
-             strips_up + strips_down + down.ksplit + 1 <= kMaxStrips;
-  if (mp.fused) {
-    mp.down = down;
-    mp.up_partial = kCounterBytes;
-    const size_t up_bytes =
-        mp.up.ksplit > 1 ? align_up((size_t)mp.up.ksplit * 2 * M * I * 4) : 0;
-    mp.down_partial = mp.up_partial + up_bytes;
-    const size_t down_bytes =
-        mp.down.ksplit > 1 ? align_up((size_t)mp.down.ksplit * M * H * 4) : 0;
-    mp.hidden = mp.down_partial + down_bytes;
-  } else {
-    const size_t a = qmv_workspace(M, H, I, 2, group_size, bits);
-    const size_t b = qmv_workspace(M, I, H, 1, group_size, bits);
-    const size_t split = align_up(a > b ? a : b);
-    mp.hidden = split > kCounterBytes ? split : kCounterBytes;
-  }
+  mp.hidden = split > kCounterBytes ? split : kCounterBytes;
   mp.bytes = mp.hidden + align_up((size_t)M * I * 2);
   return mp;
 }
@@ -801,67 +758,13 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
       !down_w || !down_scales || !down_biases)
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null pointer");
   const MlpPlan mp = plan_mlp(M, H, I, group_size, bits);
-  char* ws = static_cast<char*>(workspace);
-  void* h = ws + mp.hidden;
-  if (!mp.fused) {
-    // [counters + split-K partials | hidden activation]: the counters stay at offset 0.
-    st = affine_swiglu_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
-                            h, M, H, I, group_size, bits, dtype, workspace, mp.hidden, stream,
-                            up_layout);
-    if (st) return st;
-    return affine_qmv_impl(op, h, down_w, down_scales, down_biases, residual, y, M, I, H,
-                           group_size, bits, dtype, workspace, mp.hidden, stream, down_layout);
-  }
-  // [counters: gate/up strips | down strips | ready[] | done][gate/up partials]
-  // [down partials][hidden activation]
-  uint32_t* counters = reinterpret_cast<uint32_t*>(ws);
-  const int strips_up = I / 32, strips_down = H / 32;
-  mt::QmvParams up{}, down{};
-  up.x = static_cast<const uint16_t*>(x);
-  up.w[0] = gate_w;
-  up.w[1] = up_w;
-  up.s[0] = static_cast<const uint16_t*>(gate_scales);
-  up.s[1] = static_cast<const uint16_t*>(up_scales);
-  up.b[0] = static_cast<const uint16_t*>(gate_biases);
-  up.b[1] = static_cast<const uint16_t*>(up_biases);
-  up.y = static_cast<uint16_t*>(h);
-  up.partial = reinterpret_cast<float*>(ws + mp.up_partial);
-  up.counters = counters;
-  up.M = M;
-  up.K = H;
-  up.N = I;
-  up.ksplit = mp.up.ksplit;
-  up.steps_per_split = mp.up.steps_per_split;
-  up.strips = strips_up;
-  down.x = static_cast<const uint16_t*>(h);
-  down.w[0] = down_w;
-  down.s[0] = static_cast<const uint16_t*>(down_scales);
-  down.b[0] = static_cast<const uint16_t*>(down_biases);
-  down.residual = static_cast<const uint16_t*>(residual);
-  down.y = static_cast<uint16_t*>(y);
-  down.partial = reinterpret_cast<float*>(ws + mp.down_partial);
-  down.counters = counters + strips_up;
-  down.M = M;
-  down.K = I;
-  down.N = H;
-  down.ksplit = mp.down.ksplit;
-  down.steps_per_split = mp.down.steps_per_split;
-  down.strips = strips_down;
-  up.G = down.G = group_size;
-  up.group_shift = down.group_shift = __builtin_ctz((unsigned)(group_size / 64));
-  set_layout(up, up_layout, bits);
-  set_layout(down, down_layout, bits);
-  mt::MlpLink link{};
-  link.ready = counters + strips_up + strips_down;
-  link.done = link.ready + mp.down.ksplit;
-  link.hstrips_per_split = 2 * mp.down.steps_per_split;
-  link.down_blocks = strips_down * mp.down.ksplit;
-  link.prefetch_at = 0;
-  if (const char* env = std::getenv("METILE_AMD_MLP_PREFETCH_AT")) link.prefetch_at = std::atoi(env);
-  const hipError_t e = mt::launch_affine_mlp_fused(up, down, link, bits, dtype,
-                                                   static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, op);
-  return MT_OK;
+  void* h = static_cast<char*>(workspace) + mp.hidden;
+  st = affine_swiglu_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h,
+                          M, H, I, group_size, bits, dtype, workspace, mp.hidden, stream,
+                          up_layout);
+  if (st) return st;
+  return affine_qmv_impl(op, h, down_w, down_scales, down_biases, residual, y, M, I, H,
+                         group_size, bits, dtype, workspace, mp.hidden, stream, down_layout);
 }
 
 }  // namespace

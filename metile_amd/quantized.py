@@ -48,12 +48,20 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     Calls on one stream are ordered, so they may share it; the kernels leave its counter
     region zeroed after each call. A buffer that is outgrown is kept, not freed, so that graphs
     captured over it stay valid.
+
+    A buffer is never created or grown during graph capture: its zero fill would only be
+    recorded into that graph, not run, and a later call or graph on the stream would find it
+    uninitialised. Run the call once on the capturing stream, outside capture, first.
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
            _stream_handle(device))
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "metile_amd: this stream has no workspace large enough for the call; run it "
+                    "once on the capturing stream outside graph capture before capturing it")
             size = max(nbytes, 1 << 20, 2 * buf.numel() if buf is not None else 0)
             if buf is not None:
                 _retired.append(buf)
@@ -195,9 +203,9 @@ def affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, up_s
 
 
 def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
-    """``down(swiglu(values)) (+ residual)`` through one C-ABI call: one kernel launch for up
-    to 16 rows (gate/up and down workgroups of one grid, handing the hidden activation over
-    through the workspace), two launches above that.
+    """``down(swiglu(values)) (+ residual)`` through one C-ABI call: the fused gate/up SwiGLU
+    launch, then the down projection (with the residual epilogue) over the hidden activation,
+    which stays in the workspace.
 
     ``gate``/``up``/``down`` are ``(weight, scales, biases)`` triples; gate/up ``[I, H]``,
     down ``[H, I]``, gate and up in one code layout (MLX rows or ``affine_repack``'s), down in
@@ -251,12 +259,19 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
 def affine_dequantize(weight, scales, biases, *, group_size=64, bits=4):
     """Bit-exact fp32 ``q * s + b`` as a ``[N, K]`` float32 tensor
     (``kernels/affine_qmv.py:41-51``)."""
-    _require_device(weight, scales, biases)
-    code = _dtype_code(scales.dtype)
-    if biases is None or biases.dtype != scales.dtype or biases.shape != scales.shape:
+    if biases is None:
         raise ValueError("dequantize requires biases matching the scales")
+    if bits not in (4, 8):
+        raise ValueError("dequantize supports 4- and 8-bit codes")
+    if weight.ndim != 2 or scales.ndim != 2:
+        raise ValueError("expected packed weight and matching two-dimensional parameters")
     n = weight.shape[0]
     k = weight.shape[1] * 32 // bits
+    if (group_size < 1 or k % group_size or tuple(scales.shape) != (n, k // group_size)
+            or biases.dtype != scales.dtype or tuple(biases.shape) != tuple(scales.shape)):
+        raise ValueError("dequantize received incompatible quantization parameters")
+    _require_device(weight, scales, biases)
+    code = _dtype_code(scales.dtype)
     out = torch.empty(n, k, dtype=torch.float32, device=weight.device)
     w = _as_u32(weight)
     s, b = scales.contiguous(), biases.contiguous()
@@ -548,7 +563,7 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
 
     def bucket(values):
         rows = values.numel() // values.shape[-1]
-        return _tuning.token_bucket(_tuning.dispatch_rows(max(rows, 1), group_size)[0])
+        return _tuning.row_bucket(_tuning.dispatch_rows(max(rows, 1), group_size)[0])
 
     def stages(values):
         key = bucket(values)

@@ -4,9 +4,10 @@ Every C-ABI call plans itself from its shape (split-K, column strips, kernel). T
 were measured at the BASELINE shapes; for any other shape this module measures the plans the
 library lists for it (``mt_affine_qmv_plan_candidates``, ``mt_affine_gemm_plan_candidates``) and
 installs the fastest (``mt_affine_*_plan_set``), so that later calls of that shape take it. The
-decision is written to a JSON cache keyed by everything that can change it, as the reference's
-tuner and cache do (``metile/runtime/cache.py:12-56``; keys ``mlx_quantized.py:1393-1449``;
-tournament ``metile/tuning/tournament.py:45-94``; selection ``mlx_quantized.py:1225-1253,1275-1336``).
+decision is appended to a persistent log keyed by everything that can change it, the role the
+reference's tuner and cache play (``metile/runtime/cache.py:12-56``; keys
+``mlx_quantized.py:1393-1449``; tournament ``metile/tuning/tournament.py:21-94``; selection
+``mlx_quantized.py:1225-1253,1275-1336``).
 
 What differs from the reference, by design:
 
@@ -17,8 +18,8 @@ What differs from the reference, by design:
 * Candidates are timed as the hot path runs: each plan's dispatches are captured once in a HIP
   graph over enough copies of the weights (``COLD_BYTES``, more than twice the 256 MB Infinity
   Cache) that every dispatch streams its weights from HBM, and the graphs are replayed in a
-  rotating, alternately reversed order (``round_robin``), then the finalists head to head against
-  the baseline (``confirm_pairwise``).
+  shuffled order (``screen``), then the finalists head to head against the baseline in ABBA
+  blocks (``head_to_head``); both rank on an upper quantile of the samples (``tail_quantile``).
 * Every candidate's result must pass the reference tuner's fidelity gate
   (``affine_swiglu_compatible``) against the planner plan's result before it is timed.
 * A weight can be held in either code layout (MLX rows, or ``affine_repack``'s step-major
@@ -35,30 +36,31 @@ decisions still apply).
 from __future__ import annotations
 
 import ctypes
+import fcntl
 import hashlib
 import json
+import math
 import os
-import platform
+import random
 import statistics
-import tempfile
 import threading
-from contextlib import suppress
-from dataclasses import asdict, dataclass
+from dataclasses import asdict, astuple, dataclass
 from pathlib import Path
 
 import torch
 
 from . import _lib
 
-TUNER_VERSION = 1
+TUNER_VERSION = 2
 SWITCH_MARGIN = 0.02
 TIE_TOLERANCE = 0.0025
 FINALIST_SLACK = 1.10
-ROUNDS = 7
-CONFIRM_ROUNDS = 15
+TAIL_QUANTILE = 0.75
+SCREEN_ROUNDS = 7
+ABBA_BLOCKS = 8
 COLD_BYTES = 600 << 20
 MAX_COPIES = 256
-CACHE_FILE = "affine-plans-v1.json"
+CACHE_FILE = "affine-plans-v2.jsonl"
 
 _LAYOUT_MLX, _LAYOUT_REPACKED = 0, 1
 _LAYOUT_NAMES = {_LAYOUT_MLX: "mlx", _LAYOUT_REPACKED: "repacked"}
@@ -67,53 +69,77 @@ _KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register",
 _KERNEL_CODES = {v: k for k, v in _KERNELS.items()}
 
 
-# ---- cache files (restating metile/runtime/cache.py:12-56) -------------------------------------
+# ---- decision log ------------------------------------------------------------------------------
+# Decisions are appended, one JSON object per line, to a log that is never rewritten: the last
+# line of a key wins. An append holds an exclusive lock on the file and a read a shared one
+# (fcntl.flock), so tuning processes that share the cache keep each other's decisions, and a
+# reader never sees half a line. Keys are readable (the op and the shape) with a short hash of
+# everything else that can change the decision (the device, the library and tuner sources, the
+# candidate list and the tuner's policy).
 
 
-def cache_root() -> Path:
-    """The cache directory (not created here): ``METILE_AMD_CACHE_DIR``, else
-    ``$XDG_CACHE_HOME/metile_amd``, else ``~/.cache/metile_amd`` (``~/Library/Caches`` on macOS)."""
-    override = os.environ.get("METILE_AMD_CACHE_DIR")
-    if override:
-        return Path(override).expanduser()
-    if platform.system() == "Darwin":
-        return Path.home() / "Library" / "Caches" / "metile_amd"
-    xdg = os.environ.get("XDG_CACHE_HOME")
-    return Path(xdg).expanduser() / "metile_amd" if xdg else Path.home() / ".cache" / "metile_amd"
+def cache_dir() -> Path:
+    """``METILE_AMD_CACHE_DIR``, else ``$XDG_CACHE_HOME/metile_amd``, else
+    ``~/.cache/metile_amd`` (not created here)."""
+    explicit = os.environ.get("METILE_AMD_CACHE_DIR")
+    if explicit:
+        return Path(explicit).expanduser()
+    base = os.environ.get("XDG_CACHE_HOME") or os.path.join(os.path.expanduser("~"), ".cache")
+    return Path(base).expanduser() / "metile_amd"
 
 
 def cache_path() -> Path:
-    return cache_root() / CACHE_FILE
+    return cache_dir() / CACHE_FILE
 
 
-def stable_digest(payload) -> str:
-    """SHA-256 of the canonical JSON of ``payload`` (key order and spacing do not matter)."""
-    text = json.dumps(payload, sort_keys=True, separators=(",", ":"), default=str)
-    return hashlib.sha256(text.encode()).hexdigest()
-
-
-def read_json(path: Path, default):
-    """The JSON at ``path``, or ``default`` when it is missing, unreadable or malformed."""
+def load_decisions(path: Path | None = None) -> dict:
+    """``{key: entry}`` of the log at ``path`` (default ``cache_path()``), the last line of each
+    key winning; lines that do not parse are skipped, a missing file reads as empty."""
+    path = path or cache_path()
     try:
-        with path.open(encoding="utf-8") as f:
-            return json.load(f)
-    except (OSError, ValueError, TypeError):
-        return default
+        f = open(path, "rb")
+    except OSError:
+        return {}
+    out = {}
+    with f:
+        fcntl.flock(f.fileno(), fcntl.LOCK_SH)
+        try:
+            data = f.read()
+        finally:
+            fcntl.flock(f.fileno(), fcntl.LOCK_UN)
+    for line in data.splitlines():
+        try:
+            rec = json.loads(line)
+        except ValueError:
+            continue
+        if isinstance(rec, dict) and isinstance(rec.get("key"), str):
+            out[rec["key"]] = rec.get("entry")
+    return out
 
 
-def atomic_write_json(path: Path, payload) -> None:
-    """Replace ``path`` with ``payload`` so that readers see the old or the new file, whole."""
+def append_decision(key: str, entry: dict, path: Path | None = None) -> None:
+    """Append ``{key, entry}`` as one line under an exclusive lock."""
+    path = path or cache_path()
     path.parent.mkdir(parents=True, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(prefix=f".{path.name}.", dir=path.parent)
+    line = json.dumps({"key": key, "entry": entry}, separators=(",", ":"), default=str) + "\n"
+    fd = os.open(path, os.O_WRONLY | os.O_APPEND | os.O_CREAT, 0o644)
     try:
-        with os.fdopen(fd, "wb") as f:
-            f.write(json.dumps(payload, indent=2, sort_keys=True).encode() + b"\n")
-            f.flush()
-            os.fsync(f.fileno())
-        os.replace(tmp, path)
+        fcntl.flock(fd, fcntl.LOCK_EX)
+        try:
+            os.write(fd, line.encode())
+            os.fsync(fd)
+        finally:
+            fcntl.flock(fd, fcntl.LOCK_UN)
     finally:
-        with suppress(FileNotFoundError):
-            os.unlink(tmp)
+        os.close(fd)
+
+
+def decision_key(op: str, shape: dict, context) -> str:
+    """``op:field=value,...#hash``: the shape in clear, ``context`` (anything else the decision
+    depends on; its ``repr`` must be deterministic) as a 96-bit BLAKE2b hash."""
+    h = hashlib.blake2b(digest_size=12)
+    h.update(repr(context).encode())
+    return op + ":" + ",".join(f"{k}={shape[k]}" for k in sorted(shape)) + "#" + h.hexdigest()
 
 
 def disk_cache_enabled() -> bool:
@@ -124,9 +150,12 @@ def tuning_enabled() -> bool:
     return os.environ.get("METILE_AMD_DISABLE_TUNING") != "1"
 
 
-def token_bucket(rows: int) -> int:
-    """Rows rounded up to a power of two (the library keys installed plans the same way)."""
-    return 1 << max(rows - 1, 0).bit_length()
+def row_bucket(rows: int) -> int:
+    """The smallest power of two at or above ``rows`` (the library keys installed plans by it)."""
+    bucket = 1
+    while bucket < rows:
+        bucket *= 2
+    return bucket
 
 
 # ---- plans ---------------------------------------------------------------------------------------
@@ -234,43 +263,68 @@ def clear_plans() -> None:
         _decided_layouts.clear()
 
 
-# ---- tournament (restating metile/tuning/tournament.py:45-94) ----------------------------------
+# ---- timing and ranking -------------------------------------------------------------------------
+# Screening replays every candidate once per round in a fresh random order (a fixed seed per
+# round), so that no candidate keeps a place or a neighbour. The decision then times each
+# finalist against the baseline alone, in ABBA order (baseline, candidate, candidate, baseline:
+# a drift that is linear over the four cancels), and takes the candidate's time relative to
+# the baseline in each block. Both stages rank on an upper quantile (TAIL_QUANTILE) of the
+# samples rather than their median: a kernel that is fast when conditions line up but slow
+# most of the time must not win on its good samples.
 
 
-def round_robin(candidates, rounds, measure):
-    """``{key: [seconds, ...]}``: every candidate ``(key, runner)`` timed once per round, the
-    order rotated by one each round and reversed every other round, so that no candidate keeps
-    a position or a neighbour."""
-    candidates = list(candidates)
-    samples = {key: [] for key, _ in candidates}
-    for index in range(rounds):
-        shift = index % len(candidates) if candidates else 0
-        ordered = candidates[shift:] + candidates[:shift]
-        if index & 1:
-            ordered.reverse()
-        for key, runner in ordered:
+def tail_quantile(samples, q=None) -> float:
+    """The ``q`` quantile (default ``TAIL_QUANTILE``) of ``samples``, interpolating linearly
+    between order statistics."""
+    q = TAIL_QUANTILE if q is None else q
+    values = sorted(samples)
+    if not values:
+        raise ValueError("tail_quantile of no samples")
+    pos = q * (len(values) - 1)
+    i = math.floor(pos)
+    j = min(i + 1, len(values) - 1)
+    return values[i] + (values[j] - values[i]) * (pos - i)
+
+
+def screen(candidates, rounds, measure, seed=0):
+    """``{key: [seconds, ...]}``: each ``(key, runner)`` timed once per round, in an order
+    shuffled anew every round."""
+    items = list(candidates)
+    samples = {key: [] for key, _ in items}
+    rng = random.Random(seed)
+    for _ in range(rounds):
+        order = items[:]
+        rng.shuffle(order)
+        for key, runner in order:
             samples[key].append(measure(runner))
     return samples
 
 
-def confirm_pairwise(candidates, baseline, rounds, measure):
-    """``{key: seconds}``: each candidate timed alternately with ``baseline`` alone, ranked by
-    its median ratio to the baseline in that pairing (drift between pairings cancels), and
-    given back as that ratio times the median of the baseline's pairing medians."""
-    candidates = list(candidates)
-    base = next(c for c in candidates if c[0] == baseline)
-    others = [c for c in candidates if c[0] != baseline]
-    if not others:
-        return {baseline: statistics.median(round_robin([base], rounds, measure)[baseline])}
-    ratios, base_times = {}, []
-    for cand in others:
-        s = round_robin([base, cand], rounds, measure)
-        b = statistics.median(s[baseline])
-        base_times.append(b)
-        ratios[cand[0]] = statistics.median(s[cand[0]]) / b
-    reference = statistics.median(base_times)
+def head_to_head(candidates, baseline, blocks, measure):
+    """``{key: seconds}`` for the finalists ``candidates`` (which include ``baseline``): each
+    other candidate is timed against the baseline alone in ``blocks`` ABBA blocks; its score is
+    the tail quantile of its per-block time ratios to the baseline, given back in seconds as
+    that ratio times the median of all the baseline's samples."""
+    items = dict(candidates)
+    base_runner = items[baseline]
+    base_samples, ratios = [], {}
+    for key, runner in items.items():
+        if key == baseline:
+            continue
+        per_block = []
+        for _ in range(blocks):
+            b0 = measure(base_runner)
+            c0 = measure(runner)
+            c1 = measure(runner)
+            b1 = measure(base_runner)
+            base_samples += [b0, b1]
+            per_block.append((c0 + c1) / (b0 + b1))
+        ratios[key] = tail_quantile(per_block)
+    if not base_samples:
+        base_samples = [measure(base_runner) for _ in range(2 * blocks)]
+    reference = statistics.median(base_samples)
     out = {baseline: reference}
-    out.update({key: r * reference for key, r in ratios.items()})
+    out.update({key: ratio * reference for key, ratio in ratios.items()})
     return out
 
 
@@ -312,23 +366,23 @@ def _device_identity(device) -> dict:
 
 
 def _persistent_key(device, op, shape: dict, candidates) -> str:
-    return stable_digest({
-        **_device_identity(device),
-        "op": op,
-        **shape,
-        "candidates": [asdict(c) for c in candidates],
-        "tuner": TUNER_VERSION,
-        "switch_margin": SWITCH_MARGIN,
-        "cold_bytes": COLD_BYTES,
-    })
+    identity = _device_identity(device)
+    context = (sorted(identity.items()), [astuple(c) for c in candidates], TUNER_VERSION,
+               SWITCH_MARGIN, TAIL_QUANTILE, COLD_BYTES)
+    return decision_key(op, shape, context)
+
+
+def _read_entry(key):
+    if not disk_cache_enabled():
+        return None
+    entry = load_decisions().get(key)
+    return entry if isinstance(entry, dict) and "plan" in entry else None
 
 
 def _read_decision(key, plan_type):
     """(found, plan): ``plan`` is None when the planner's plan was kept."""
-    if not disk_cache_enabled():
-        return False, None
-    entry = read_json(cache_path(), {}).get(key)
-    if not isinstance(entry, dict) or "plan" not in entry:
+    entry = _read_entry(key)
+    if entry is None:
         return False, None
     if entry["plan"] is None:
         return True, None
@@ -339,13 +393,13 @@ def _read_decision(key, plan_type):
 
 
 def _write_decision(key, plan, record) -> None:
-    if not disk_cache_enabled():
-        return
-    payload = read_json(cache_path(), {})
-    if not isinstance(payload, dict):
-        payload = {}
-    payload[key] = {"plan": None if plan is None else asdict(plan), **record}
-    atomic_write_json(cache_path(), payload)
+    if disk_cache_enabled():
+        append_decision(key, {"plan": None if plan is None else asdict(plan), **record})
+
+
+def cached_decisions() -> list:
+    """Every decision in the log (the entries, newest per key)."""
+    return [e for e in load_decisions().values() if isinstance(e, dict)]
 
 
 def _tensor_bytes(*tensors) -> int:
@@ -399,13 +453,13 @@ def _tournament(bench, graphs, copies, cost, baseline=_BASELINE):
     entries = list(graphs.items())
     for _, g in entries:  # one untimed replay each: clocks and caches in the steady state
         measure(g)
-    provisional = {k: statistics.median(v) for k, v in round_robin(entries, ROUNDS, measure).items()}
+    provisional = {k: tail_quantile(v) for k, v in screen(entries, SCREEN_ROUNDS, measure).items()}
     best = min(provisional.values())
     alternatives = [k for k in provisional if k != baseline]
     fastest_alt = min(alternatives, key=provisional.__getitem__) if alternatives else None
     finalists = [(k, g) for k, g in entries
                  if provisional[k] <= best * FINALIST_SLACK or k in (baseline, fastest_alt)]
-    timings = confirm_pairwise(finalists, baseline, CONFIRM_ROUNDS, measure)
+    timings = head_to_head(finalists, baseline, ABBA_BLOCKS, measure)
     timings = {k: t / copies for k, t in timings.items()}
     return timings, choose(timings, baseline, cost)
 
@@ -509,7 +563,7 @@ def _tune_qmv_layouts(values, weight_sets, group_size, bits):
 
 
 def _qmv_shape(rows, k, n, group_size, bits, nproj, dtype) -> dict:
-    return {"rows": token_bucket(rows), "input_features": k, "output_features": n,
+    return {"rows": row_bucket(rows), "input_features": k, "output_features": n,
             "group_size": group_size, "bits": bits, "nproj": nproj, "dtype": str(dtype)}
 
 
@@ -519,7 +573,7 @@ def dispatch_rows(rows: int, group_size: int) -> list[int]:
     chunk = 16 if group_size == 32 else 32
     out = []
     for r in (min(rows, chunk), rows % chunk if rows > chunk else 0):
-        if r and token_bucket(r) not in {token_bucket(v) for v in out}:
+        if r and row_bucket(r) not in {row_bucket(v) for v in out}:
             out.append(r)
     return out
 
@@ -541,7 +595,7 @@ def ensure_qmv_plans(values, weights, *, group_size, bits, autotune=True, retune
     out = {}
     with _lock:
         for rows in dispatch_rows(x.shape[0], group_size):
-            mem = ("qmv", values.device.index, token_bucket(rows), k, n, group_size, bits, nproj,
+            mem = ("qmv", values.device.index, row_bucket(rows), k, n, group_size, bits, nproj,
                    values.dtype)
             if mem in _decided and not retune:
                 out[rows] = _decided[mem]
@@ -594,7 +648,7 @@ def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retun
     rows = dispatch_rows(x.shape[0], group_size)[0]
     chosen = names[0]
     with _lock:
-        mem = ("qmv", values.device.index, token_bucket(rows), k, n, group_size, bits, nproj,
+        mem = ("qmv", values.device.index, row_bucket(rows), k, n, group_size, bits, nproj,
                values.dtype)
         lmem = (*mem, tuple(names))
         if lmem in _decided_layouts and not retune:
@@ -630,7 +684,7 @@ def _read_layout_decision(key):
     found, plan = _read_decision(key, QmvPlan)
     if not found:
         return False, None, None
-    entry = read_json(cache_path(), {}).get(key, {})
+    entry = _read_entry(key) or {}
     return True, plan, entry.get("layout")
 
 
@@ -692,11 +746,11 @@ def ensure_gemm_plan(values, weight, scales, biases, *, group_size, autotune=Tru
     rows = x.shape[0]
     n = weight.shape[0]
     with _lock:
-        mem = ("gemm", values.device.index, token_bucket(rows), k, n, group_size, values.dtype)
+        mem = ("gemm", values.device.index, row_bucket(rows), k, n, group_size, values.dtype)
         if mem in _decided and not retune:
             return _decided[mem]
         candidates = gemm_plan_candidates(rows, k, n, group_size)
-        shape = {"rows": token_bucket(rows), "input_features": k, "output_features": n,
+        shape = {"rows": row_bucket(rows), "input_features": k, "output_features": n,
                  "group_size": group_size, "bits": 4, "dtype": str(values.dtype)}
         key = _persistent_key(values.device, "affine_matmul", shape, candidates)
         found, plan = (False, None) if retune else _read_decision(key, GemmPlan)

@@ -417,7 +417,10 @@ PINNED_BY = {
     "affine_qmv": "reference KAT tests/test_affine_quantized.py:120-163 (seed 211), torch CPU",
     "silu_mul": "special cases g=0, g>>0, g<<0, and torch.nn.functional.silu",
     "affine_mlp": "composition of pinned parts; torch CPU end-to-end",
-    "dense_swiglu": "torch CPU typed-rounding restatement; g=0 and saturation special cases",
+    "dense_swiglu": "exhaustive bf16 gate sweep within 3 ulps of fp64 silu(g)*u (u on rounding "
+                    "ties); g=0 -> 0, g>=8 -> round(g*u), g<=-89 -> 0, -89<g<=-20 bounded by "
+                    "|g u| e^g; dot products rounded before the epilogue; a reversed sign "
+                    "select fails these; torch CPU typed ops agree bit for bit",
     "dense_residual_qmv": "torch CPU (bf16 round of fp32 dot, then bf16 add)",
     "tolerance_error": "planted mistakes (dropped bias term, transposed weight) fail it",
 }

@@ -58,6 +58,8 @@ CASES = [  # (K, N, group, bits, dtype, nproj, residual)
     (8960, 1536, 64, 4, "f16", 1, False),
     (1536, 8960, 64, 4, "bf16", 2, False),   # the gate/up shape: 48 chunks, most lanes idle
     (1536, 8960, 128, 4, "f16", 2, False),
+    (1536, 8960, 64, 4, "bf16", 1, True),    # config 0: one projection, column groups
+    (1536, 8960, 64, 4, "f16", 1, False),
     (4864, 896, 32, 8, "bf16", 1, True),     # 8 bits, groups of 32
     (1024, 1536, 64, 8, "f16", 2, False),
     (2624, 640, 32, 4, "bf16", 1, False),    # 82 chunks: ragged last pass at every width

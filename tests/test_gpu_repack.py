@@ -77,11 +77,8 @@ def test_swiglu_repacked_equals_native_and_nax_entry(m, bits, g, dtype):
         assert _same(one, mt.mlx_affine_qmv(x, *gate, group_size=g, bits=bits))
 
 
-@pytest.mark.parametrize("path", ["split", "fused"])
 @pytest.mark.parametrize("m", [1, 3, 16, 33])
-def test_mlp_repacked_equals_native(monkeypatch, path, m):
-    if path == "fused":
-        monkeypatch.setenv("METILE_AMD_MLP_PATH", "fused")
+def test_mlp_repacked_equals_native(m):
     h, i = 1536, 8960
     gate = affine_to_torch(O.make_affine_weight(i, h, 4, 64, 5, 10), "bf16")
     up = affine_to_torch(O.make_affine_weight(i, h, 4, 64, 5, 12), "bf16")
@@ -90,7 +87,7 @@ def test_mlp_repacked_equals_native(monkeypatch, path, m):
     r = act_to_torch(O.make_activations(m, h, 5, tensor_id=3), "bf16")
     want = mt.affine_mlp(x, gate, up, down, residual=r)
     rp = [(mt.affine_repack(t[0]), t[1], t[2]) for t in (gate, up, down)]
-    for _ in range(2):  # the second call finds the hand-off counters cleared again
+    for _ in range(2):  # the second call finds the split-K counters cleared again
         got = mt.affine_mlp(x, *rp, residual=r)
         assert _same(got, want)
     # a layout per stage (mt_affine_mlp_layouts): gate/up in one, down in the other

@@ -182,3 +182,23 @@ def test_mixed_code_layouts_are_rejected():
         mt.affine_swiglu(x, w, s, b, packed, s, b)
     with pytest.raises(ValueError, match="gate and up weights must share one code layout"):
         mt.affine_mlp(x, (w, s, b), (packed, s, b), (dw, ds, db))
+
+
+def test_dequantize_validates_scale_and_code_shapes():
+    """Scales and biases must be [N, K / group_size] for the codes given, or the kernel would
+    index past them."""
+    w, s, b = _affine(64, 256)
+    with pytest.raises(ValueError, match="requires biases"):
+        mt.affine_dequantize(w, s, None)
+    with pytest.raises(ValueError, match="incompatible quantization parameters"):
+        mt.affine_dequantize(w, s, b, group_size=32)  # scales hold 4 groups, 8 needed
+    with pytest.raises(ValueError, match="incompatible quantization parameters"):
+        mt.affine_dequantize(w, s, b[:, :2])
+    with pytest.raises(ValueError, match="incompatible quantization parameters"):
+        mt.affine_dequantize(w[:32], s, b)
+    with pytest.raises(ValueError, match="two-dimensional"):
+        mt.affine_dequantize(w[0], s, b)
+    with pytest.raises(ValueError, match="4- and 8-bit"):
+        mt.affine_dequantize(w, s, b, bits=3)
+    with pytest.raises(ValueError, match="ROCm device tensors"):
+        mt.affine_dequantize(w, s, b)  # valid shapes, host tensors

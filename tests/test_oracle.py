@@ -249,6 +249,113 @@ def test_dense_swiglu_matches_torch_typed_ops():
     np.testing.assert_array_equal(got, out.view(torch.int16).numpy().view(np.uint16))
 
 
+def _dense_epilogue(left_bits, right_bits, fn=None):
+    """Drive ``O.dense_swiglu`` with x = e0 (one 1.0), so that the gate and up dot products are
+    exactly the given bf16 values and only the typed epilogue acts on them."""
+    fn = fn or O.dense_swiglu
+    n, k = left_bits.size, 64
+    x = np.zeros((1, k), np.uint16)
+    x[0, 0] = 0x3F80
+    g = np.zeros((n, k), np.uint16)
+    u = np.zeros((n, k), np.uint16)
+    g[:, 0], u[:, 0] = left_bits, right_bits
+    return fn(x, g, u)[0]
+
+
+def _reversed_select(x, g, u):
+    """A planted mistake: the sign select reversed (equivalently exp(-|g|) in place of
+    exp(|g|)), i.e. g * sigmoid(-g) * u: the oracle applied to -g, negated."""
+    return O.from_f32(-O.to_f32(O.dense_swiglu(x, O.from_f32(-O.to_f32(g, "bf16"), "bf16"), u),
+                                "bf16"), "bf16")
+
+
+def _bf16_grid(lo, hi):
+    """Every finite bf16 value v with lo <= |v| <= hi, and zero (bit patterns, values)."""
+    b = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(invalid="ignore"):
+        v = O.bf16_bits_to_f32(b).astype(np.float64)
+    keep = np.isfinite(v) & (((np.abs(v) >= lo) & (np.abs(v) <= hi)) | (v == 0))
+    return b[keep], v[keep]
+
+
+U_SWEEP = [1.0, 1.5, -3.0, 0.0234375, 1.0078125, -0.7109375, 113.0]
+
+
+def _ulps_from_exact(got_bits, exact):
+    mag = np.maximum(np.abs(exact), 2.0 ** -126)
+    ulp = np.ldexp(1.0, (np.floor(np.log2(mag)) - 7).astype(np.int64))
+    return np.abs(O.bf16_bits_to_f32(got_bits).astype(np.float64) - exact) / ulp
+
+
+def test_dense_swiglu_within_three_ulps_of_exact_silu_exhaustive():
+    """Every bf16 gate value in [2^-100, 80] (and 0) against fp64 silu(g) * u for u values whose
+    products land on bf16 rounding ties. The typed chain rounds six times (exp, 1 + e, the
+    reciprocal, 1 - y, g * sig, act * u), each by at most half an ulp, and 1 - y (y <= 1/2)
+    does not amplify y's error relative to the result, so it stays within 3 ulps of the exact
+    value (measured maximum 2.6)."""
+    left, lv = _bf16_grid(2.0 ** -100, 80.0)
+    for uval in U_SWEEP:
+        ub = O.f32_to_bf16_bits(np.full(left.size, uval, np.float32))
+        exact = lv / (1.0 + np.exp(-lv)) * uval
+        err = _ulps_from_exact(_dense_epilogue(left, ub), exact)
+        assert err.max() <= 3.0, (uval, float(err.max()), float(lv[np.argmax(err)]))
+        bad = _ulps_from_exact(_dense_epilogue(left, ub, _reversed_select), exact)
+        assert bad.max() > 100.0, uval  # the planted mistake fails the same bound
+
+
+def test_dense_swiglu_special_cases_zero_and_saturation():
+    """g = 0 gives exactly 0; g >= 8 gives exactly round(g * u) (1 - y rounds to 1 once
+    y < 2^-9, i.e. g > ln 511); g <= -89 gives exactly 0 (exp overflows, y = 0); for
+    -89 < g <= -20 the result has the sign of -u and magnitude at most |g u| e^g (1 + 2^-6)."""
+    for uval in U_SWEEP:
+        left, lv = _bf16_grid(8.0, 1.0e30)
+        pos = lv > 0
+        left, lv = left[pos], lv[pos]
+        ub = O.f32_to_bf16_bits(np.full(left.size, uval, np.float32))
+        with np.errstate(over="ignore"):
+            want = O.f32_to_bf16_bits((lv * uval).astype(np.float32))
+        np.testing.assert_array_equal(_dense_epilogue(left, ub), want)
+        assert not np.array_equal(_dense_epilogue(left, ub, _reversed_select), want)
+
+        def us(count):
+            return O.f32_to_bf16_bits(np.full(count, uval, np.float32))
+
+        zero = np.array([0x0000, 0x8000], np.uint16)
+        out = O.bf16_bits_to_f32(_dense_epilogue(zero, us(2)))
+        np.testing.assert_array_equal(out, [0.0, 0.0])
+
+        left, lv = _bf16_grid(89.0, 3.0e38)
+        left = left[lv < 0]
+        out = O.bf16_bits_to_f32(_dense_epilogue(left, us(left.size)))
+        np.testing.assert_array_equal(out, np.zeros(left.size))
+
+        left, lv = _bf16_grid(20.0, 88.9)
+        neg = lv < 0
+        left, lv = left[neg], lv[neg]
+        out = O.bf16_bits_to_f32(_dense_epilogue(left, us(left.size))).astype(np.float64)
+        bound = np.abs(lv * uval) * np.exp(lv) * (1 + 2.0 ** -6)
+        assert np.all(np.abs(out) <= bound)
+        assert np.all((out == 0) | (np.sign(out) == -np.sign(uval)))
+
+
+def test_dense_swiglu_rounds_the_dot_products_before_the_epilogue():
+    """g = 1 + 2^-8 + 2^-12 (a sum of exact products, not a bf16 value) must enter the epilogue
+    as bf16(g) = 1 + 2^-7: the result equals the epilogue of 1 + 2^-7 exactly, and differs from
+    that of 1.0 (the value a truncation would give)."""
+    x = np.zeros((1, 64), np.uint16)
+    x[0, :3] = O.f32_to_bf16_bits(np.array([1.0, 1.0, 1.0], np.float32))
+    g = np.zeros((1, 64), np.uint16)
+    g[0, :3] = O.f32_to_bf16_bits(np.array([1.0, 2.0 ** -8, 2.0 ** -12], np.float32))
+    u = np.zeros((1, 64), np.uint16)
+    u[0, 0] = 0x3FC0  # 1.5
+    got = O.dense_swiglu(x, g, u)[0]
+    up = O.f32_to_bf16_bits(np.array([1.0 + 2.0 ** -7], np.float32))
+    one = O.f32_to_bf16_bits(np.array([1.0], np.float32))
+    u1 = np.array([0x3FC0], np.uint16)
+    assert got[0] == _dense_epilogue(up, u1)[0]
+    assert got[0] != _dense_epilogue(one, u1)[0]
+
+
 def test_dense_residual_rounds_projection_then_sum():
     k, n, m = 128, 32, 3
     x = O.make_activations(m, k, 2)

@@ -1,14 +1,17 @@
-"""The tuner's host side, no GPU: the decision cache files and keys, the tournament's order and
-arithmetic, the selection rule, and the plan table of the C ABI (candidate lists, validation,
-installation, bucketing, workspace sizes), which is host-only code.
+"""The tuner's host side, no GPU: the decision log and keys, the screening order, the ABBA
+head-to-head arithmetic and its tail-quantile ranking, the selection rule, and the plan table of
+the C ABI (candidate lists, validation, installation, bucketing, workspace sizes), which is
+host-only code.
 
-The cache and tournament restate ``metile/runtime/cache.py:12-56`` and
-``metile/tuning/tournament.py:45-94``; the selection rule is this build's (a margin over the
+The tuner fills the role of ``metile/runtime/cache.py:12-56`` and
+``metile/tuning/tournament.py:21-94`` with its own design (an append-only, locked decision
+log; shuffled screening; ABBA pairs); the selection rule is this build's (a margin over the
 planner's plan, ties to the fewest workgroups)."""
 
 from __future__ import annotations
 
 import json
+import multiprocessing
 import os
 
 import pytest
@@ -18,37 +21,57 @@ from metile_amd import build, tuning
 from metile_amd.tuning import GemmPlan, QmvPlan
 
 
-# ---- cache files ---------------------------------------------------------------------------------
+# ---- decision log --------------------------------------------------------------------------------
 
 
-def test_cache_root_precedence(monkeypatch, tmp_path):
+def test_cache_dir_precedence(monkeypatch, tmp_path):
     monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path / "a"))
     monkeypatch.setenv("XDG_CACHE_HOME", str(tmp_path / "x"))
-    assert tuning.cache_root() == tmp_path / "a"
+    assert tuning.cache_dir() == tmp_path / "a"
     monkeypatch.delenv("METILE_AMD_CACHE_DIR")
-    assert tuning.cache_root() == tmp_path / "x" / "metile_amd"
+    assert tuning.cache_dir() == tmp_path / "x" / "metile_amd"
     monkeypatch.delenv("XDG_CACHE_HOME")
-    assert tuning.cache_root().parts[-2:] == (".cache", "metile_amd")
+    assert tuning.cache_dir().parts[-2:] == (".cache", "metile_amd")
 
 
-def test_stable_digest_ignores_key_order_and_sees_values():
-    a = tuning.stable_digest({"x": 1, "y": [1, 2], "z": {"b": 2, "a": 1}})
-    b = tuning.stable_digest({"z": {"a": 1, "b": 2}, "y": [1, 2], "x": 1})
-    assert a == b and len(a) == 64
-    assert a != tuning.stable_digest({"x": 1, "y": [2, 1], "z": {"b": 2, "a": 1}})
+def test_decision_key_is_readable_and_hashes_the_context():
+    shape = {"rows": 1, "input_features": 1536}
+    a = tuning.decision_key("affine_qmv", shape, ("lib", [1, 2]))
+    assert a.startswith("affine_qmv:input_features=1536,rows=1#") and len(a.split("#")[1]) == 24
+    assert a == tuning.decision_key("affine_qmv", dict(reversed(list(shape.items()))),
+                                    ("lib", [1, 2]))
+    assert a != tuning.decision_key("affine_qmv", shape, ("lib", [2, 1]))
+    assert a != tuning.decision_key("affine_matmul", shape, ("lib", [1, 2]))
 
 
-def test_json_round_trip_and_unreadable_files(tmp_path):
-    path = tmp_path / "d" / "c.json"
-    assert tuning.read_json(path, {"missing": True}) == {"missing": True}
-    tuning.atomic_write_json(path, {"k": {"plan": None}})
-    assert tuning.read_json(path, {}) == {"k": {"plan": None}}
-    assert os.listdir(path.parent) == ["c.json"]  # no temporary file left behind
-    path.write_text("{not json")
-    assert tuning.read_json(path, "default") == "default"
+def test_log_appends_last_entry_wins_and_skips_torn_lines(tmp_path):
+    path = tmp_path / "d" / "log.jsonl"
+    assert tuning.load_decisions(path) == {}
+    tuning.append_decision("k", {"plan": None}, path)
+    tuning.append_decision("j", {"plan": {"tile": 64}}, path)
+    tuning.append_decision("k", {"plan": {"tile": 128}}, path)
+    with open(path, "a") as f:
+        f.write('{"key": "torn", "entry"')  # a line cut short
+    assert tuning.load_decisions(path) == {"k": {"plan": {"tile": 128}},
+                                           "j": {"plan": {"tile": 64}}}
+    assert len(path.read_text().splitlines()) == 4  # appended, never rewritten
 
 
-def test_decisions_round_trip_through_the_cache(monkeypatch, tmp_path):
+def _append_many(args):
+    path, who = args
+    for i in range(50):
+        tuning.append_decision(f"{who}-{i}", {"plan": None, "i": i}, path)
+
+
+def test_concurrent_writers_keep_every_decision(tmp_path):
+    path = tmp_path / "log.jsonl"
+    with multiprocessing.get_context("spawn").Pool(4) as pool:
+        pool.map(_append_many, [(path, w) for w in range(4)])
+    got = tuning.load_decisions(path)
+    assert len(got) == 200 and all(got[f"{w}-{i}"]["i"] == i for w in range(4) for i in range(50))
+
+
+def test_decisions_round_trip_through_the_log(monkeypatch, tmp_path):
     monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
     plan = QmvPlan("staged", 3, 544, 1)
     tuning._write_decision("k1", plan, {"planner_us": 9.0})
@@ -56,10 +79,9 @@ def test_decisions_round_trip_through_the_cache(monkeypatch, tmp_path):
     assert tuning._read_decision("k1", QmvPlan) == (True, plan)
     assert tuning._read_decision("k2", QmvPlan) == (True, None)
     assert tuning._read_decision("k3", QmvPlan) == (False, None)
-    data = json.loads(tuning.cache_path().read_text())
-    data["k4"] = {"plan": {"tile": 64}}  # malformed: missing a field
-    tuning.atomic_write_json(tuning.cache_path(), data)
+    tuning.append_decision("k4", {"plan": {"tile": 64}})  # malformed: missing a field
     assert tuning._read_decision("k4", GemmPlan) == (False, None)
+    assert {e.get("planner_us") for e in tuning.cached_decisions()} == {9.0, 5.0, None}
     monkeypatch.setenv("METILE_AMD_DISABLE_DISK_CACHE", "1")
     assert tuning._read_decision("k1", QmvPlan) == (False, None)
     tuning._write_decision("k5", plan, {})
@@ -67,9 +89,9 @@ def test_decisions_round_trip_through_the_cache(monkeypatch, tmp_path):
     assert tuning._read_decision("k5", QmvPlan) == (False, None)
 
 
-def test_token_bucket_and_dispatch_rows():
-    assert [tuning.token_bucket(r) for r in (1, 2, 3, 5, 8, 9, 17, 32)] == [1, 2, 4, 8, 8, 16, 32,
-                                                                           32]
+def test_row_bucket_and_dispatch_rows():
+    assert [tuning.row_bucket(r) for r in (1, 2, 3, 5, 8, 9, 17, 32)] == [1, 2, 4, 8, 8, 16, 32,
+                                                                         32]
     assert tuning.dispatch_rows(1, 64) == [1]
     assert tuning.dispatch_rows(32, 64) == [32]
     assert tuning.dispatch_rows(64, 64) == [32]
@@ -78,29 +100,58 @@ def test_token_bucket_and_dispatch_rows():
     assert tuning.dispatch_rows(48, 32) == [16]
 
 
-# ---- tournament and selection --------------------------------------------------------------------
+# ---- timing and ranking --------------------------------------------------------------------------
 
 
-def test_round_robin_rotates_and_reverses():
+def test_tail_quantile_interpolates_order_statistics():
+    assert tuning.tail_quantile([4.0, 1.0, 3.0, 2.0, 5.0]) == 4.0
+    assert tuning.tail_quantile([1.0, 2.0], 0.75) == pytest.approx(1.75)
+    assert tuning.tail_quantile([7.0]) == 7.0
+    with pytest.raises(ValueError):
+        tuning.tail_quantile([])
+
+
+def test_tail_quantile_rejects_a_bimodal_kernel_the_median_would_pick():
+    """The case that motivates ranking on a tail (metile/tuning/tournament.py:21-42): a kernel
+    quick when conditions line up (1643 us) but slower most of the time (2874 us) against a
+    steady baseline (2047-2073 us). Its median beats the baseline; its upper quantile does
+    not, and the baseline is kept."""
+    bimodal = [1643.0, 1650.0, 1700.0, 1800.0, 2874.0, 2874.0, 2900.0]
+    steady = [2047.0, 2052.0, 2060.0, 2066.0, 2073.0, 2050.0, 2061.0]
+    med = {"base": sorted(steady)[3], "x": sorted(bimodal)[3]}
+    assert tuning.choose(med, "base", lambda k: 0) == "x"  # what a median ranking would do
+    tail = {"base": tuning.tail_quantile(steady), "x": tuning.tail_quantile(bimodal)}
+    assert tuning.choose(tail, "base", lambda k: 0) == "base"
+
+
+def test_screen_shuffles_each_round_and_times_everyone():
     order = []
-    cands = [("a", "a"), ("b", "b"), ("c", "c")]
-    samples = tuning.round_robin(cands, 4, lambda r: order.append(r) or len(order))
-    assert order == ["a", "b", "c",  # shift 0
-                     "a", "c", "b",  # shift 1 (b c a), reversed
-                     "c", "a", "b",  # shift 2
-                     "c", "b", "a"]  # shift 0, reversed
-    assert {k: len(v) for k, v in samples.items()} == {"a": 4, "b": 4, "c": 4}
+    cands = [(k, k) for k in "abcdef"]
+    samples = tuning.screen(cands, 6, lambda r: order.append(r) or float(len(order)))
+    rounds = [order[i:i + 6] for i in range(0, 36, 6)]
+    assert all(sorted(r) == list("abcdef") for r in rounds)
+    assert len({tuple(r) for r in rounds}) > 1  # not one fixed order
+    assert {k: len(v) for k, v in samples.items()} == dict.fromkeys("abcdef", 6)
+    again = []
+    tuning.screen(cands, 6, lambda r: again.append(r) or 0.0)
+    assert again == order  # seeded: reproducible
 
 
-def test_confirm_pairwise_rebuilds_times_from_ratios():
-    # each pairing drifts by a different factor; the ratios cancel it
-    drift = iter([1.0, 1.0, 1.0, 1.0, 2.0, 2.0, 2.0, 2.0])
+def test_head_to_head_runs_abba_and_cancels_linear_drift():
+    calls = []
     times = {"base": 10.0, "x": 8.0, "y": 12.0}
-    got = tuning.confirm_pairwise([("base", "base"), ("x", "x"), ("y", "y")], "base", 2,
-                                  lambda r: times[r] * next(drift))
-    assert got["base"] == pytest.approx(15.0)  # median of the pairings' baselines (10, 20)
-    assert got["x"] == pytest.approx(0.8 * 15.0)
-    assert got["y"] == pytest.approx(1.2 * 15.0)
+
+    def measure(r):
+        calls.append(r)
+        return times[r] * (1.0 + 0.01 * len(calls))  # a clock that drifts linearly
+
+    got = tuning.head_to_head([("base", "base"), ("x", "x"), ("y", "y")], "base", 3, measure)
+    assert calls[:4] == ["base", "x", "x", "base"]
+    assert len(calls) == 2 * 3 * 4
+    # ABBA: the drift of each block cancels in (c0 + c1) / (b0 + b1)
+    ref = got["base"]
+    assert got["x"] / ref == pytest.approx(0.8, rel=1e-12)
+    assert got["y"] / ref == pytest.approx(1.2, rel=1e-12)
 
 
 def test_choose_needs_the_margin_and_breaks_ties_by_cost():
@@ -137,13 +188,13 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
 
     for dtype in (torch.bfloat16, torch.float16):
         planner = tuning.qmv_plan(rows, k, n, g, bits, nproj, dtype)
-        if tuning.token_bucket(rows) == rows:
+        if tuning.row_bucket(rows) == rows:
             assert planner in cands
     gemv = [c for c in cands if c.kernel == "gemv"]
     # GEMV plans exist for up to 4 rows: 2 and 4 columns per workgroup, and for each number of
     # passes over K's 16-byte chunks the fewest waves (of 64 lanes) that make it; with more
     # than one pass, at most 8 of projections x columns x rows (registers)
-    bucket = tuning.token_bucket(rows)
+    bucket = tuning.row_bucket(rows)
     chunks = k * bits // 128
 
     def groups(w):  # column groups per workgroup: one pass over K in whole rows of 16 lanes
