@@ -248,3 +248,43 @@ def test_golden_swiglu_and_mlp():
                       affine_to_torch((d["dw"], d["ds"], d["db"]), "bf16"),
                       residual=act_to_torch(d["residual"], "bf16"))
     _report("golden mlp", torch_to_act(y, "bf16"), d["ref"], min_exact=0.85)
+
+
+def test_workspace_is_never_created_inside_graph_capture():
+    """A split-K call (the down projection at 8 rows: 5 K splits) on a stream without a
+    workspace raises under capture instead of recording the workspace's zero fill into the
+    graph; after one call outside capture, graphs captured on that stream replay correctly in
+    any order, with eager calls between replays."""
+    k, n, m = 8960, 1536, 8
+    w = affine_to_torch(O.make_affine_weight(n, k, 4, 64, 9, 10), "bf16")
+    x = act_to_torch(O.make_activations(m, k, 9), "bf16")
+    x2 = act_to_torch(O.make_activations(m, k, 9, tensor_id=4), "bf16")
+    want1 = mt.affine_qmv(x, *w)
+    want2 = mt.affine_qmv(x2, *w)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    g0 = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="outside graph capture"):
+        with torch.cuda.graph(g0, stream=stream):
+            mt.affine_qmv(x, *w)
+    with torch.cuda.stream(stream):
+        mt.affine_qmv(x, *w)  # creates the stream's workspace, outside capture
+    stream.synchronize()
+    outs = {}
+    graphs = []
+    for key, xin in (("a", x), ("b", x2)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            outs[key] = mt.affine_qmv(xin, *w)
+        graphs.append(g)
+    for _ in range(3):
+        graphs[1].replay()
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs["b"].view(torch.int16), want2.view(torch.int16))
+        assert torch.equal(outs["a"].view(torch.int16), want1.view(torch.int16))
+        with torch.cuda.stream(stream):
+            mid = mt.affine_qmv(x2, *w)
+        stream.synchronize()
+        assert torch.equal(mid.view(torch.int16), want2.view(torch.int16))

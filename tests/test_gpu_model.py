@@ -18,7 +18,6 @@
 
 from __future__ import annotations
 
-import json
 
 import numpy as np
 import pytest
@@ -214,7 +213,7 @@ def test_tuned_graph_fusion_decodes_the_same_tokens(monkeypatch, tmp_path):
         base, patched, calls = _decode_patched(model, mt.patch_graph_fusion,
                                                "_execute_quantized_mlp")
         assert calls == {"plain": 0, "residual": 3 * 25}
-        decisions = json.loads(tuning.cache_path().read_text()).values()
+        decisions = tuning.load_decisions().values()
         assert {(d["rows"], d["nproj"]) for d in decisions} >= {(1, 1), (1, 2), (16, 1), (16, 2)}
         _assert_same_decode("qwen2 tuned", base, patched)
     finally:

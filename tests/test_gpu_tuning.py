@@ -13,7 +13,6 @@
 from __future__ import annotations
 
 import functools
-import json
 
 import numpy as np
 import pytest
@@ -154,7 +153,7 @@ def test_tuner_decides_persists_and_reloads(monkeypatch, tmp_path):
     planner = tuning.qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16)
 
     decision = tuning.ensure_qmv_plans(xt, packed, group_size=64, bits=4)
-    entries = json.loads(tuning.cache_path().read_text())
+    entries = tuning.load_decisions()
     assert len(entries) == 1
     record = next(iter(entries.values()))
     print(f"[tuner swiglu M=1] planner {record['planner']} {record['planner_us']} us, "
@@ -190,7 +189,7 @@ def test_layout_decision_persists_and_reloads(monkeypatch, tmp_path):
     layouts = {"repacked": packed, "mlx": mlx}
     layout = tuning.ensure_qmv_layout(ht, layouts, group_size=64, bits=4)
     assert layout in layouts
-    entries = json.loads(tuning.cache_path().read_text())
+    entries = tuning.load_decisions()
     assert len(entries) == 1
     record = next(iter(entries.values()))
     print(f"[tuner down M=1 layouts] planner {record['planner']} {record['planner_us']} us "
@@ -224,13 +223,13 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     ts = [affine_to_torch(w, "bf16") for w in (gate, up, down)]
     ex = mt.mlx_affine_mlp_executor(xt, *ts[0], *ts[1], *ts[2], rt)
     _check("tuned mlp", torch_to_act(ex(xt, rt), "bf16"), ref, min_exact=0.85)
-    entries = json.loads(tuning.cache_path().read_text())
+    entries = tuning.load_decisions()
     assert {e["nproj"] for e in entries.values()} == {1, 2}  # both stages decided
     assert all(e["layout"] in ("mlx", "repacked") for e in entries.values())
     # a one-row call: its row bucket gets its own plans and layouts on first use
     ref1, _ = O.affine_mlp(x[:1], gate, up, down, 64, 4, residual=res[:1])
     _check("tuned mlp, one row", torch_to_act(ex(xt[:1], rt[:1]), "bf16"), ref1, min_exact=0.85)
-    rows = {(e["rows"], e["nproj"]) for e in json.loads(tuning.cache_path().read_text()).values()}
+    rows = {(e["rows"], e["nproj"]) for e in tuning.load_decisions().values()}
     assert {(1, 1), (1, 2), (4, 1), (4, 2)} <= rows
     # the prefill GEMM through the tuned reference entry
     w = affine_to_torch(O.make_affine_weight(1536, 1024, 4, 64, 9, 10), "bf16")
@@ -238,7 +237,7 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     xp = act_to_torch(O.make_activations(200, 1024, 9), "bf16")
     y = mt.mlx_affine_matmul(xp, aw)
     assert mt.accuracy_compatible(y, mt.native_affine_matmul(xp, aw))
-    gemm = [e for e in json.loads(tuning.cache_path().read_text()).values()
+    gemm = [e for e in tuning.load_decisions().values()
             if e["op"] == "affine_matmul"]
     assert len(gemm) == 1
     print(f"[tuner gemm 200x1024x1536] planner {gemm[0]['planner']} {gemm[0]['planner_us']} us, "

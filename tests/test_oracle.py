@@ -356,6 +356,71 @@ def test_dense_swiglu_rounds_the_dot_products_before_the_epilogue():
     assert got[0] != _dense_epilogue(one, u1)[0]
 
 
+def _f32_dots_reversed(x, w):
+    """fp32 dot products summed in reverse K order (another summation order than the oracle's
+    fp64 one), as a GPU accumulation might give them."""
+    xf = O.to_f32(x, "bf16")
+    wf = O.to_f32(w, "bf16")
+    acc = np.zeros((xf.shape[0], wf.shape[0]), np.float32)
+    for k in range(xf.shape[1] - 1, -1, -1):
+        acc += xf[:, k:k + 1] * wf[None, :, k]
+    return acc
+
+
+def test_budget_error_accepts_the_typed_chains_and_other_summation_orders():
+    """The oracle's typed outputs score ~0 against the exact results with their rounding budget,
+    and so do typed chains fed fp32 dot products summed in another order (which flip some
+    intermediate roundings: a one-ulp flip of the output would be several 1e-3 of the typed
+    reference, but scores only the accumulation noise here)."""
+    k, n, m = 2048, 96, 4
+    x = O.make_activations(m, k, 2)
+    g = O.make_dense_weight(n, k, 2, 10)
+    u = O.make_dense_weight(n, k, 2, 11)
+    d = O.make_dense_weight(n, k, 2, 12)
+    r = O.make_activations(m, n, 2, tensor_id=3)
+    ex, bud = O.dense_swiglu_exact(x, g, u)
+    assert O.budget_tolerance_error(O.dense_swiglu(x, g, u), ex, bud) <= 1e-9
+    exr, budr = O.dense_residual_exact(x, d, r)
+    assert O.budget_tolerance_error(O.dense_residual_qmv(x, d, r), exr, budr) <= 1e-9
+    ex0, bud0 = O.dense_residual_exact(x, d, None)
+    assert O.budget_tolerance_error(O.dense_residual_qmv(x, d, None), ex0, bud0) <= 1e-9
+
+    left = O.f32_to_bf16_bits(_f32_dots_reversed(x, g))
+    right = O.f32_to_bf16_bits(_f32_dots_reversed(x, u))
+    typed = np.stack([_dense_epilogue(left[i], right[i]) for i in range(m)])
+    assert O.budget_tolerance_error(typed, ex, bud) < 1e-5
+    proj = O.bf16_bits_to_f32(O.f32_to_bf16_bits(_f32_dots_reversed(x, d)))
+    typed_r = O.f32_to_bf16_bits(proj + O.bf16_bits_to_f32(r))
+    assert O.budget_tolerance_error(typed_r, exr, budr) < 1e-5
+
+
+def test_budget_error_over_every_bf16_gate_value():
+    left, _ = _bf16_grid(2.0 ** -100, 80.0)
+    for uval in U_SWEEP:
+        ub = O.f32_to_bf16_bits(np.full(left.size, uval, np.float32))
+        x = np.zeros((1, 64), np.uint16)
+        x[0, 0] = 0x3F80
+        gw = np.zeros((left.size, 64), np.uint16)
+        uw = np.zeros((left.size, 64), np.uint16)
+        gw[:, 0], uw[:, 0] = left, ub
+        ex, bud = O.dense_swiglu_exact(x, gw, uw)
+        assert O.budget_tolerance_error(O.dense_swiglu(x, gw, uw), ex, bud) <= 1e-9, uval
+
+
+def test_budget_error_fails_planted_mistakes():
+    k, n, m = 512, 64, 3
+    x = O.make_activations(m, k, 2)
+    g = O.make_dense_weight(n, k, 2, 10)
+    u = O.make_dense_weight(n, k, 2, 11)
+    r = O.make_activations(m, n, 2, tensor_id=3)
+    ex, bud = O.dense_swiglu_exact(x, g, u)
+    assert O.budget_tolerance_error(_reversed_select(x, g, u), ex, bud) > 2e-3
+    assert O.budget_tolerance_error(O.dense_swiglu(x, g, u)[:, ::-1], ex, bud) > 2e-3
+    exr, budr = O.dense_residual_exact(x, g, r)
+    assert O.budget_tolerance_error(O.dense_residual_qmv(x, g, None), exr, budr) > 2e-3
+    assert O.budget_tolerance_error(O.dense_residual_qmv(x, u, r), exr, budr) > 2e-3
+
+
 def test_dense_residual_rounds_projection_then_sum():
     k, n, m = 128, 32, 3
     x = O.make_activations(m, k, 2)
