@@ -81,6 +81,21 @@ int mt_affine_mlp(const void* x, const uint32_t* gate_w, const void* gate_scales
                   int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
                   void* stream);
 
+/* mt_affine_mlp without a caller workspace, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. The workspace lives in a 16 MiB device array inside the library
+ * (one per GPU, held until the process ends); a call whose mt_affine_mlp_workspace_bytes exceeds
+ * 16 MiB fails with MT_ERR_WORKSPACE. It allocates nothing (no hipMalloc, no allocating library
+ * call); the first call on a device clears the array's counter region with a small kernel on
+ * `stream`. Every call on a GPU shares that array: calls that overlap on one GPU (other
+ * streams, or a graph captured over this call replayed while another runs) race. Same arguments
+ * (minus the workspace) and results as mt_affine_mlp, bit for bit. */
+int mt_affine_mlp_noalloc(const void* x, const uint32_t* gate_w, const void* gate_scales,
+                          const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+                          const void* up_biases, const uint32_t* down_w, const void* down_scales,
+                          const void* down_biases, const void* residual, void* y, int M, int H,
+                          int I, int group_size, int bits, int dtype, void* stream);
+
 /* out[n, k] = q[n, k] * s[n, k/G] + b[n, k/G] in fp32 (bit-exact dequantization, the decode
  * step of kernels/affine_qmv.py:41-51). Any group_size dividing K with K % (32/bits) == 0. */
 int mt_affine_dequantize(const uint32_t* w_q, const void* scales, const void* biases,

@@ -57,6 +57,8 @@ SIGNATURES = {
     "mt_affine_mlp_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "mt_affine_mlp": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                            _I, _P, _Z, _P]),
+    "mt_affine_mlp_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                   _I, _I, _P]),
     "mt_affine_dequantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "mt_affine_quantize": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "mt_affine_repack": (_I, [_P, _P, _I, _I, _I, _P]),

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "affine_qmv.h"
+#include "capi_internal.h"
 #include "dense_qmv.h"
 #include "affine_gemm.h"
 #include "affine_quantize.h"
@@ -768,6 +769,32 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
 }
 
 }  // namespace
+
+// Entry points in other source files that bring their own workspace (noalloc.hip) reach the MLP
+// path and the error slot through these.
+namespace mt {
+
+int set_last_error(int status, const std::string& msg) { return fail(status, msg); }
+
+size_t affine_mlp_workspace(int M, int H, int I, int group_size, int bits) {
+  if (check_affine("mt_affine_mlp", M, H, I, group_size, bits, MT_BF16) ||
+      check_affine("mt_affine_mlp", M, I, H, group_size, bits, MT_BF16))
+    return 0;
+  return plan_mlp(M, H, I, group_size, bits).bytes;
+}
+
+int affine_mlp(const char* op, const void* x, const uint32_t* gate_w, const void* gate_scales,
+               const void* gate_biases, const uint32_t* up_w, const void* up_scales,
+               const void* up_biases, const uint32_t* down_w, const void* down_scales,
+               const void* down_biases, const void* residual, void* y, int M, int H, int I,
+               int group_size, int bits, int dtype, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  return affine_mlp_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
+                         down_w, down_scales, down_biases, residual, y, M, H, I, group_size,
+                         bits, dtype, workspace, workspace_bytes, stream, kLayoutMlx, kLayoutMlx);
+}
+
+}  // namespace mt
 
 extern "C" {
 
