@@ -206,10 +206,11 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
 /* How one small-row dispatch runs: the kernel, the number of K splits, the number of column
  * strips (workgroup columns; N/32 for the register kernel, N/32 to 2N/32 for the staged kernel)
  * and the strips per workgroup (1 or 2, staged kernel only). The GEMV kernel (up to 4 rows)
- * never splits K: its strips are N/4 or N/2 (4 or 2 columns per workgroup), `tiles` holds its
- * waves per workgroup (1 to 8) and `order` how workgroups take column groups (0: in index
- * order; 1: dealt out to the 8 XCDs in runs of adjacent groups). `order` is 0 for the other
- * kernels. */
+ * never splits K: its strips are its workgroups, N / (columns x column groups) with 2, 4 or
+ * 8 columns per group (8: one projection of up to 2 rows) and, when one pass of its lanes covers
+ * K in whole rows of 16 lanes, several column groups per workgroup; `tiles` holds its waves per
+ * workgroup (1 to 8) and `order` how workgroups take column groups (0: in index order; 1:
+ * dealt out to the 8 XCDs in runs of adjacent groups). `order` is 0 for the other kernels. */
 typedef enum mt_qmv_kernel {
   MT_QMV_STAGED = 1,
   MT_QMV_REGISTER = 2,
@@ -271,10 +272,11 @@ const char* mt_source_digest(void);
 
 /* ---- measurement -------------------------------------------------------------------------- */
 
-/* Reads `bytes` from `p` with `blocks` workgroups of 16-byte loads and writes one word per
- * block to `sink` (at least `blocks` words): the streaming-read ceiling of one launch. No
- * counterpart entry point in the reference; it is the analogue of its measured
- * streaming-read constant (metile/target/agx.py:38). */
+/* Reads `bytes` from `p` with `blocks` workgroups of 256 threads issuing 16-byte loads (grid
+ * stride, 8 in flight per thread) and no reduction: the streaming-read ceiling of one launch.
+ * `sink` (at least `blocks` words) is written only when a thread's XOR of its data equals a
+ * fixed sentinel, which keeps the loads alive. No counterpart entry point in the reference; it
+ * is the analogue of its measured streaming-read constant (metile/target/agx.py:38). */
 int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream);
 
 #ifdef __cplusplus

@@ -3,7 +3,8 @@
 // staged kernel (kernels/affine_qmv.py:57-214; mlx_affine_qmv, mlx_affine_swiglu,
 // metile/backends/mlx_quantized.py:691-751,1645-1720).
 //
-// A workgroup owns COLS output columns (2 or 4) and all of K, so no partial sum leaves it. Its
+// A workgroup owns COLS output columns (2, 4, or 8 for one projection of one or two rows) and
+// all of K, so no partial sum leaves it. Its
 // lanes (1 to 8 waves; the plan picks the fewest that cover K in a given number of passes) split
 // K into 16-byte code chunks (32 codes at 4 bits, 16 at 8 bits): lane t takes the chunks t,
 // t + lanes, t + 2 lanes, ... of every one of the workgroup's columns, and loads the activations
@@ -11,7 +12,8 @@
 // chunks fill whole rows of 16 lanes, a workgroup covers several groups of COLS columns, lane t
 // taking chunk t % chunks of group t / chunks (K = 1536 at 4 bits: 48 chunks, three waves serve
 // four groups with no idle lane). A chunk's codes are unpacked to exact
-// 16-bit floats offset + q in K order and dotted with the activations two at a time (fp32
+// 16-bit floats offset + q (4-bit codes in the paired order of each word, the activations
+// re-ordered to match) and dotted with the activations two at a time (fp32
 // accumulate), together with the activations' sum; the group's affine terms are applied in
 // fp32 as in the staged kernel: acc += s * sum_k x_k (offset + q_k) + (b - offset * s) sum_k x_k.
 // Chunks never straddle a group (groups are 32 codes or more and chunk-aligned).
@@ -30,27 +32,42 @@ namespace {
 // adjacent column groups), and neighbouring columns share their XCD's L2 for the cache lines
 // they have in common (scale and bias rows do not start on line boundaries). Any order is
 // correct; which is faster depends on the shape (measured: the one-row down projection 4.41 ->
-// 4.30 us with this order, the one-row SwiGLU 6.99 -> 7.14 us), so the plan picks it. Groups
-// past the last multiple of 8 keep their index.
-__device__ __forceinline__ int gemv_column_group(int b, int groups) {
+// 4.30 us with this order, the one-row SwiGLU 6.99 -> 7.14 us), so the plan picks it. `whole`
+// (from the host: the grid rounded down to a multiple of 8, or 0 under order 0) workgroups are
+// dealt out; the rest keep their index. Branch-free, with no read of the grid size: a branch
+// here had split the kernel's argument loads into three dependent rounds before the first
+// memory request.
+__device__ __forceinline__ int gemv_column_group(int b, int whole) {
   constexpr int kXcds = 8;
-  const int whole = groups - groups % kXcds;
-  if (b >= whole) return b;
-  return (b % kXcds) * (whole / kXcds) + b / kXcds;
+  const int dealt = (b % kXcds) * (whole / kXcds) + b / kXcds;
+  return b < whole ? dealt : b;
 }
 
+// How a one-pass workgroup lays its column groups over its lanes.
+//  * kOneGroup: one group of COLS columns; its chunks span the waves (cross-wave sums in LDS).
+//  * kStraddle: several groups, lane t taking group t / chunks, chunk t % chunks; groups may
+//    span two waves (cross-wave sums in LDS).
+//  * kWaveGroups (a column's chunks fit in one wave): every wave holds whole groups (64 / chunks
+//    of them when chunks is a multiple of 16, else one), so each group's sums stay inside its
+//    wave: DPP within rows of 16 lanes, then the group's row sums read with readlane and added
+//    in row order. No wave waits for another (no LDS, no barrier); the order of every addition
+//    is the same as the LDS path's, so the results are the same bit for bit.
+enum GemvLayout : int { kOneGroup = 0, kStraddle = 1, kWaveGroups = 2 };
+
 // ONE_PASS: every lane has at most one chunk per column (K / chunk <= lanes), so no second
-// pass is held in registers (more waves fit on a CU). GROUPS: the workgroup covers several
-// column groups (one pass only); a separate instance, so that one-group workgroups keep their
+// pass is held in registers (more waves fit on a CU). LAYOUT: see GemvLayout (one pass only
+// for kStraddle and kWaveGroups); separate instances, so that one-group workgroups keep their
 // columns wave-uniform and issue their loads without the per-lane group arithmetic.
-template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS, bool GROUPS>
-__global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams p) {
+template <int BITS, int DT, int ROWS, int NPROJ, int COLS, bool ONE_PASS, int LAYOUT>
+__global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const QmvParams args) {
+  // All arguments in one batch of scalar loads: left to itself the compiler fetched them in
+  // three dependent rounds (a full scalar-memory wait each) before the first load was issued.
+  const QmvParams p = preload_args(args);
   constexpr int kChunks = BITS / 2;        // 16-byte chunks per column and 64-wide K step
   constexpr int kCodes = 128 / BITS;       // codes per chunk
   constexpr int kXLoads = kCodes / 8;      // 16-byte activation loads per chunk and row
   constexpr int kOut = NPROJ * COLS * ROWS;
   constexpr float kOff = CodeOffset<BITS, DT>::value;
-  __shared__ float red[kGemvMaxWaves][kOut][4];  // per wave, output and row of 16 lanes
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -60,13 +77,21 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   const int M = p.M, K = p.K, N = p.N;
   const int chunks = K / kCodes;
   // One pass over short K: the workgroup covers `groups` column groups, lane t group t / chunks
-  // and chunk t % chunks (lanes past the last group load nothing). Otherwise one group.
-  static_assert(ONE_PASS || !GROUPS, "column groups need one pass");
-  const int groups = GROUPS ? affine_gemv_groups(K, BITS, waves) : 1;
-  const int gi = GROUPS ? tid / chunks : 0;
-  const int kc0 = GROUPS ? tid % chunks : tid;
-  const bool lane_on = !GROUPS || gi < groups;
-  const int wg = p.order ? gemv_column_group(blockIdx.x, gridDim.x) : blockIdx.x;
+  // and chunk t % chunks (lanes past the last group load nothing). Otherwise one group. The
+  // quotient comes from a float reciprocal: (t + 1/2) / chunks stays at least 1 / (2 chunks)
+  // from an integer, far beyond the reciprocal's error for t and chunks below 512.
+  static_assert(ONE_PASS || LAYOUT == kOneGroup, "column groups need one pass");
+  constexpr bool GROUPS = LAYOUT != kOneGroup;
+  const int groups = GROUPS ? p.gemv_groups : 1;
+  // kWaveGroups: groups per wave (from the host), and lane t of wave w takes group
+  // w * gpw + lane / chunks.
+  const int gpw = LAYOUT == kWaveGroups ? p.gemv_groups_per_wave : 0;
+  const int lt = LAYOUT == kWaveGroups ? lane : tid;  // position counted within the wave
+  const int gq = GROUPS ? (int)(((float)lt + 0.5f) * __builtin_amdgcn_rcpf((float)chunks)) : 0;
+  const int gi = LAYOUT == kWaveGroups ? wave * gpw + gq : gq;
+  const int kc0 = GROUPS ? lt - gq * chunks : tid;
+  const bool lane_on = !GROUPS || (LAYOUT == kWaveGroups ? gq < gpw : gi < groups);
+  const int wg = gemv_column_group(blockIdx.x, p.gemv_dealt);
   const int col0 = (wg * groups + gi) * COLS;  // this lane's first column
   const int gshift = __builtin_ctz((unsigned)p.G);
   const int groups_per_row = K >> gshift;
@@ -116,13 +141,21 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 #pragma unroll
       for (int m = 0; m < ROWS; ++m) acc[pr][j][m] = 0.0f;
 
+  // 4-bit codes are unpacked in the paired order (0,4,1,5,2,6,3,7) of each word, one AND-OR per
+  // pair of codes (unpack_u4_paired), and the activations are put in the same order once per
+  // lane (pair_order), for all of its columns.
+  const PairedConsts pc = paired_consts<DT>();
   auto compute = [&](const Stage& S) {
     float xs[ROWS];
+    u32x4 xp[ROWS][kXLoads];
 #pragma unroll
     for (int m = 0; m < ROWS; ++m) {
       xs[m] = 0.0f;
 #pragma unroll
-      for (int v = 0; v < kXLoads; ++v) xs[m] = sum8<DT>(S.x[m][v], xs[m]);
+      for (int v = 0; v < kXLoads; ++v) {
+        xs[m] = sum8<DT>(S.x[m][v], xs[m]);
+        xp[m][v] = BITS == 4 ? pair_order(S.x[m][v]) : S.x[m][v];
+      }
     }
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
@@ -132,7 +165,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 #pragma unroll
         for (int v = 0; v < kXLoads; ++v) {
           if constexpr (BITS == 4) {
-            cw[v] = unpack_u4<DT>(S.q[pr][j][v]);
+            cw[v] = unpack_u4_paired(S.q[pr][j][v], pc);
           } else {
             const u32x2 lo = unpack_u8<DT>(S.q[pr][j][2 * v]);
             const u32x2 hi = unpack_u8<DT>(S.q[pr][j][2 * v + 1]);
@@ -146,7 +179,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
           float t = 0.0f;
 #pragma unroll
           for (int v = 0; v < kXLoads; ++v) {
-            const u32x4 xv = S.x[m][v];
+            const u32x4 xv = xp[m][v];
             const u32x4 cv = cw[v];
             t = dot2<DT>(xv.x, cv.x, t);
             t = dot2<DT>(xv.y, cv.y, t);
@@ -178,39 +211,93 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   }
 
   // Rows of 16 lanes by DPP (each lane ends with its row's sum; a row never spans two groups),
-  // then a group's rows in LDS, in row order.
+  // then a group's rows in row order: read from other lanes of the wave (kWaveGroups) or
+  // through LDS.
+  if constexpr (LAYOUT == kWaveGroups) {
+    // Every lane ends with its row's sum; a group's rows (at most 4: a group is at most one
+    // wave) are read from their first lanes and added in row order, giving every lane the
+    // group's totals. Lane (j, m) of each group then stores output (m, column j).
+    const int rows16 = (chunks + 15) >> 4;  // rows of 16 lanes per group
 #pragma unroll
-  for (int pr = 0; pr < NPROJ; ++pr)
+    for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-    for (int j = 0; j < COLS; ++j)
+      for (int j = 0; j < COLS; ++j)
 #pragma unroll
-      for (int m = 0; m < ROWS; ++m) {
-        float v = group_sum8(acc[pr][j][m]);
-        v += dpp_read<kDppRowRor8>(v);
-        if ((lane & 15) == 0) red[wave][(pr * COLS + j) * ROWS + m][lane >> 4] = v;
+        for (int m = 0; m < ROWS; ++m) {
+          const float v = group_sum8(acc[pr][j][m]);
+          acc[pr][j][m] = v + dpp_read<kDppRowRor8>(v);
+        }
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    for (int gl = 0; gl < gpw; ++gl) {
+      float mine[NPROJ];
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr) mine[pr] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < COLS; ++j)
+#pragma unroll
+        for (int m = 0; m < ROWS; ++m) {
+#pragma unroll
+          for (int pr = 0; pr < NPROJ; ++pr) {
+            // Rows past the group add +0.0, which leaves the sum unchanged: no branches.
+            const int a = __builtin_bit_cast(int, acc[pr][j][m]);
+            float t = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float rv = __builtin_bit_cast(
+                  float, __builtin_amdgcn_readlane(a, 16 * ((gl * rows16 + r) & 3)));
+              t += r < rows16 ? rv : 0.0f;
+            }
+            if (lane == j * ROWS + m) mine[pr] = t;
+          }
+        }
+      const int j = lane / ROWS, m = lane % ROWS;
+      if (lane < COLS * ROWS && m < M) {
+        const size_t o = (size_t)m * N + (wg * groups + wave_u * gpw + gl) * COLS + j;
+        float out;
+        if constexpr (NPROJ == 2) {
+          out = silu_mul(mine[0], mine[1]);
+        } else {
+          out = mine[0];
+          if (p.residual) out += act_to_f32<DT>(p.residual[o]);
+        }
+        p.y[o] = f32_to_act<DT>(out);
       }
-  __syncthreads();
-  if (tid < groups * COLS * ROWS) {
-    const int g = tid / (COLS * ROWS), j = (tid / ROWS) % COLS, m = tid % ROWS;
-    const int r0 = GROUPS ? g * (chunks / 16) : 0;
-    const int r1 = GROUPS ? r0 + chunks / 16 : 4 * waves;
-    float v[NPROJ];
-#pragma unroll
-    for (int pr = 0; pr < NPROJ; ++pr) {
-      float s = 0.0f;
-      for (int r = r0; r < r1; ++r) s += red[r >> 2][(pr * COLS + j) * ROWS + m][r & 3];
-      v[pr] = s;
     }
-    if (m < M) {
-      const size_t o = (size_t)m * N + (wg * groups + g) * COLS + j;
-      float out;
-      if constexpr (NPROJ == 2) {
-        out = silu_mul(v[0], v[1]);
-      } else {
-        out = v[0];
-        if (p.residual) out += act_to_f32<DT>(p.residual[o]);
+  } else {
+    __shared__ float red[kGemvMaxWaves][kOut][4];  // per wave, output and row of 16 lanes
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int j = 0; j < COLS; ++j)
+#pragma unroll
+        for (int m = 0; m < ROWS; ++m) {
+          float v = group_sum8(acc[pr][j][m]);
+          v += dpp_read<kDppRowRor8>(v);
+          if ((lane & 15) == 0) red[wave][(pr * COLS + j) * ROWS + m][lane >> 4] = v;
+        }
+    __syncthreads();
+    if (tid < groups * COLS * ROWS) {
+      const int g = tid / (COLS * ROWS), j = (tid / ROWS) % COLS, m = tid % ROWS;
+      const int r0 = GROUPS ? g * (chunks / 16) : 0;
+      const int r1 = GROUPS ? r0 + chunks / 16 : 4 * waves;
+      float v[NPROJ];
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr) {
+        float s = 0.0f;
+        for (int r = r0; r < r1; ++r) s += red[r >> 2][(pr * COLS + j) * ROWS + m][r & 3];
+        v[pr] = s;
       }
-      p.y[o] = f32_to_act<DT>(out);
+      if (m < M) {
+        const size_t o = (size_t)m * N + (wg * groups + g) * COLS + j;
+        float out;
+        if constexpr (NPROJ == 2) {
+          out = silu_mul(v[0], v[1]);
+        } else {
+          out = v[0];
+          if (p.residual) out += act_to_f32<DT>(p.residual[o]);
+        }
+        p.y[o] = f32_to_act<DT>(out);
+      }
     }
   }
 }
@@ -219,16 +306,19 @@ template <int BITS, int DT, int ROWS, int NPROJ, int COLS>
 hipError_t launch_waves(const QmvParams& p, int waves, hipStream_t stream) {
   if (affine_gemv_one_pass(p.K, BITS, waves)) {
     const int groups = affine_gemv_groups(p.K, BITS, waves);
-    if (groups > 1)
-      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, true>
+    if (p.K * BITS / 128 <= 64)
+      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, kWaveGroups>
+          <<<p.N / (COLS * groups), 64 * waves, 0, stream>>>(p);
+    else if (groups > 1)
+      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, kStraddle>
           <<<p.N / (COLS * groups), 64 * waves, 0, stream>>>(p);
     else
-      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, false>
+      affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, true, kOneGroup>
           <<<p.N / COLS, 64 * waves, 0, stream>>>(p);
     return hipGetLastError();
   }
   if constexpr (affine_gemv_fits(ROWS, NPROJ, COLS, false)) {
-    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false, false>
+    affine_gemv_kernel<BITS, DT, ROWS, NPROJ, COLS, false, kOneGroup>
         <<<p.N / COLS, 64 * waves, 0, stream>>>(p);
     return hipGetLastError();
   }
@@ -239,6 +329,9 @@ template <int BITS, int DT, int ROWS, int NPROJ>
 hipError_t launch_cols(const QmvParams& p, int waves, int cols, hipStream_t stream) {
   if (cols == 2) return launch_waves<BITS, DT, ROWS, NPROJ, 2>(p, waves, stream);
   if (cols == 4) return launch_waves<BITS, DT, ROWS, NPROJ, 4>(p, waves, stream);
+  if constexpr (NPROJ == 1 && ROWS <= 2) {
+    if (cols == 8) return launch_waves<BITS, DT, ROWS, NPROJ, 8>(p, waves, stream);
+  }
   return hipErrorInvalidValue;
 }
 

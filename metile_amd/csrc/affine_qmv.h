@@ -35,6 +35,10 @@ struct QmvParams {
   int col_align;             // staged kernels: strip boundaries at multiples of this many
                              // columns (1, or a 128-byte line of repacked codes)
   int order;                 // GEMV kernel: 1 = column groups dealt out XCD by XCD
+  int gemv_groups;           // GEMV kernel: column groups per workgroup (affine_gemv_groups)
+  int gemv_groups_per_wave;  // GEMV kernel, whole groups in every wave: groups per wave
+  int gemv_dealt;            // GEMV kernel: workgroups dealt out XCD by XCD (order 1: the grid
+                             // rounded down to a multiple of 8; order 0: none)
 };
 
 // Step-major repack of MLX affine codes: the 8 * bits bytes of column n and K step t (codes
@@ -115,19 +119,24 @@ __host__ __device__ constexpr int affine_gemv_row_bucket(int rows) {
 }
 __host__ __device__ constexpr bool affine_gemv_fits(int rows, int nproj, int cols,
                                                     bool one_pass) {
-  return rows >= 1 && rows <= kGemvMaxRows && (cols == 2 || cols == 4) &&
+  return rows >= 1 && rows <= kGemvMaxRows &&
+         (cols == 2 || cols == 4 || (cols == 8 && one_pass && nproj == 1 && rows <= 2)) &&
          (one_pass || nproj * cols * affine_gemv_row_bucket(rows) <= 8);
 }
 // Whether a dispatch of K codes per column takes one pass with `waves` waves.
 __host__ __device__ constexpr bool affine_gemv_one_pass(int K, int bits, int waves) {
   return K * bits / 128 <= 64 * waves;
 }
-// Column groups (of `cols` columns each) one workgroup covers: in one pass, when a column's
-// chunks fill whole rows of 16 lanes (so DPP row sums never mix groups), as many groups as its
-// lanes hold (lane t: group t / chunks, chunk t % chunks); otherwise one. Grid: N / (cols *
-// groups) workgroups.
+// Column groups (of `cols` columns each) one workgroup covers. When a column's chunks fit in one
+// wave (at most 64), every wave holds whole groups: 64 / chunks of them when the chunks fill
+// whole rows of 16 lanes (so DPP row sums never mix groups), else one. Otherwise, in one pass,
+// when the chunks fill whole rows of 16 lanes, as many groups as the workgroup's lanes hold
+// (lane t: group t / chunks, chunk t % chunks), and else one. Grid: N / (cols * groups)
+// workgroups.
 __host__ __device__ constexpr int affine_gemv_groups(int K, int bits, int waves) {
-  return affine_gemv_one_pass(K, bits, waves) && (K * bits / 128) % 16 == 0
+  return K * bits / 128 <= 64
+             ? waves * ((K * bits / 128) % 16 == 0 ? 64 / (K * bits / 128) : 1)
+         : affine_gemv_one_pass(K, bits, waves) && (K * bits / 128) % 16 == 0
              ? 64 * waves / (K * bits / 128)
              : 1;
 }

@@ -51,7 +51,8 @@ struct Stage {
 
 
 template <int BITS, int DT, int MROWS, int NPROJ, int WAVES, int STAGES>
-__global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams p) {
+__global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams args) {
+  const QmvParams p = preload_args(args);  // all arguments in one batch of scalar loads
   constexpr int kThreads = WAVES * 64;
   constexpr float kOff = CodeOffset<BITS, DT>::value;
   constexpr int kRegs = MROWS / 2;  // accumulator registers holding rows < MROWS

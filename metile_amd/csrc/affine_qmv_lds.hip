@@ -348,7 +348,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
 // workgroup) share a CU.
 template <int BITS, int DT, int MROWS, int NPROJ, int STAGES, bool HALF, int TILES>
 __global__ __launch_bounds__(kQmvLdsWaves * 64 * TILES) __attribute__((amdgpu_waves_per_eu(4)))
-void affine_qmv_lds_kernel(const QmvParams p) {
+void affine_qmv_lds_kernel(const QmvParams args) {
+  const QmvParams p = preload_args(args);  // all arguments in one batch of scalar loads
   extern __shared__ __align__(16) unsigned char dyn_plain[];
   __shared__ int flag[TILES];
   lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, HALF, TILES>(p, blockIdx.x,

@@ -292,7 +292,8 @@ mt_qmv_plan to_public(const Plan& p) {
 // register kernel covers 32-column strips of up to 32 rows and groups of 64 or more; the staged
 // kernel up to 16 rows, N / 32 to 2 N / 32 strips (16 to 32 columns each) in workgroups of one or
 // two strips, within its LDS; every split holds at most kMaxGroupsPerSplit - 1 groups. The GEMV
-// kernel takes up to 4 rows, no K split, 2 or 4 columns per workgroup (strips = N / columns),
+// kernel takes up to 4 rows, no K split, 2, 4 or 8 columns per column group (8: one projection
+// of up to 2 rows; strips = N / (columns x column groups per workgroup)),
 // 1 to 8 waves (tiles), and when a lane has more than one chunk per column, at most 8 of
 // projections x columns x rows (more would spill registers).
 std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, int bits,
@@ -304,9 +305,9 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
     if (q.tiles < 1 || q.tiles > mt::kGemvMaxWaves)
       return "GEMV tiles (waves per workgroup) must be in 1..8";
     const int groups = mt::affine_gemv_groups(K, bits, q.tiles);
-    if (q.strips < 1 || N % (q.strips * groups) ||
-        (N / q.strips / groups != 2 && N / q.strips / groups != 4))
-      return "GEMV strips must be N/(2 groups) or N/(4 groups)";
+    const int cols = q.strips >= 1 ? N / q.strips / groups : 0;
+    if (q.strips < 1 || N % (q.strips * groups) || (cols != 2 && cols != 4 && cols != 8))
+      return "GEMV strips must be N/(2, 4 or 8 columns x groups)";
     if (q.order != 0 && q.order != 1) return "GEMV order must be 0 or 1";
     if (!mt::affine_gemv_fits(rows, nproj, N / q.strips / groups,
                               mt::affine_gemv_one_pass(K, bits, q.tiles)))
@@ -379,21 +380,26 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
         if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, st).empty()) out.push_back(st);
       }
   }
-  // GEMV: for each number of passes over K (one 16-byte chunk of codes per lane and pass), the
-  // fewest waves that make it; in one pass, also the wave counts whose lanes hold two or more
-  // whole column groups with no lane idle.
+  // GEMV: when a column's chunks fit in one wave (each wave then holds whole column groups),
+  // every wave count; otherwise, for each number of passes over K (one 16-byte chunk of codes
+  // per lane and pass), the fewest waves that make it, and in one pass also the wave counts
+  // whose lanes hold two or more whole column groups with no lane idle.
   const int chunks = K * bits / 128;
   std::vector<int> waves;
-  for (int passes = 1; passes <= 2 * mt::kGemvMaxWaves; ++passes) {
-    const int w = (chunks + 64 * passes - 1) / (64 * passes);
-    if (w <= mt::kGemvMaxWaves && (waves.empty() || waves.back() != w)) waves.push_back(w);
-    if (w == 1) break;
+  if (chunks <= 64) {
+    for (int w = 1; w <= mt::kGemvMaxWaves; ++w) waves.push_back(w);
+  } else {
+    for (int passes = 1; passes <= 2 * mt::kGemvMaxWaves; ++passes) {
+      const int w = (chunks + 64 * passes - 1) / (64 * passes);
+      if (w <= mt::kGemvMaxWaves && (waves.empty() || waves.back() != w)) waves.push_back(w);
+      if (w == 1) break;
+    }
+    for (int w = 1; w <= mt::kGemvMaxWaves; ++w)
+      if (mt::affine_gemv_groups(K, bits, w) >= 2 && (64 * w) % chunks == 0 &&
+          std::find(waves.begin(), waves.end(), w) == waves.end())
+        waves.push_back(w);
   }
-  for (int w = 1; w <= mt::kGemvMaxWaves; ++w)
-    if (mt::affine_gemv_groups(K, bits, w) >= 2 && (64 * w) % chunks == 0 &&
-        std::find(waves.begin(), waves.end(), w) == waves.end())
-      waves.push_back(w);
-  for (int cols : {4, 2})
+  for (int cols : {8, 4, 2})
     for (int w : waves)
       for (int order : {1, 0}) {
         const int per_wg = cols * mt::affine_gemv_groups(K, bits, w);
@@ -514,6 +520,9 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.strips = plan.strips;
     p.tiles = plan.kernel == MT_QMV_STAGED ? plan.tiles : 1;
     p.order = plan.order;
+    p.gemv_groups = plan.kernel == MT_QMV_GEMV ? mt::affine_gemv_groups(K, bits, plan.tiles) : 1;
+    p.gemv_groups_per_wave = plan.kernel == MT_QMV_GEMV ? p.gemv_groups / plan.tiles : 0;
+    p.gemv_dealt = plan.kernel == MT_QMV_GEMV && plan.order ? plan.strips - plan.strips % 8 : 0;
     set_layout(p, layout, bits);
     hipError_t e;
     if (plan.kernel == MT_QMV_GEMV)

@@ -67,6 +67,23 @@ __device__ __forceinline__ void store2_device(__amdgpu_buffer_rsrc_t r, uint32_t
   __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kDeviceScope);
 }
 
+// A kernel's argument block copied into scalar registers at once: every dword is read, then all
+// are pinned in SGPRs together, so the compiler issues the scalar loads in one batch with one
+// wait instead of fetching each field at its first use (which it did in several dependent
+// rounds, each a full scalar-memory latency before the kernel's first memory request).
+template <typename T>
+__device__ __forceinline__ T preload_args(const T& a) {
+  static_assert(sizeof(T) % 4 == 0, "argument block of whole dwords");
+  constexpr int kWords = sizeof(T) / 4;
+  uint32_t w[kWords];
+  __builtin_memcpy(w, &a, sizeof(T));
+#pragma unroll
+  for (int i = 0; i < kWords; ++i) __asm__ volatile("" : "+s"(w[i]));
+  T out;
+  __builtin_memcpy(&out, w, sizeof(T));
+  return out;
+}
+
 // ---- 16-bit float conversions ----------------------------------------------------------
 
 template <int DT>

@@ -50,7 +50,8 @@ __device__ __forceinline__ uint16_t typed_swiglu(float g, float u) {
 }
 
 template <int DT, int MT, int NPROJ, int STAGES>
-__global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParams p) {
+__global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParams args) {
+  const DenseParams p = preload_args(args);  // all arguments in one batch of scalar loads
   __shared__ float red[kWaves][NPROJ][32][33];
   __shared__ int last_flag;
 

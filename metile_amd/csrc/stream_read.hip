@@ -9,33 +9,31 @@ namespace mt {
 namespace {
 
 constexpr int kUnroll = 8;
+constexpr uint32_t kSentinel = 0x9E3779B9u;
 
+// Grid-stride 16-byte loads: at each step the grid reads one contiguous span of
+// gridDim.x * 4 KiB (block b its 4 KiB at b * 4 KiB), up to kUnroll steps in flight per thread.
+// Each thread XOR-folds what it read and stores it only if it equals a sentinel, which keeps the
+// loads alive without a reduction at the end: the probe is the stream alone, with no tail a
+// reduction or store would add.
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* p, uint32_t bytes,
                                                           uint32_t* sink) {
   const __amdgpu_buffer_rsrc_t r = make_rsrc(p, bytes);
-  const uint32_t per_block = ((bytes + gridDim.x - 1) / gridDim.x + 4095u) & ~4095u;
-  const uint32_t base = blockIdx.x * per_block;
-  const uint32_t end = min(bytes, base + per_block);
+  const uint32_t stride = gridDim.x * 256u * 16u;
+  uint32_t off = (blockIdx.x * 256u + threadIdx.x) * 16u;
   uint32_t acc = 0;
-  for (uint32_t off = base + threadIdx.x * 16u; off < end; off += 256u * 16u * kUnroll) {
+  for (; off + (kUnroll - 1) * stride < bytes; off += kUnroll * stride) {
     u32x4 v[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const uint32_t o = off + (uint32_t)u * 256u * 16u;
-      v[u] = load16(r, o < end ? o : kOOB);
-    }
+    for (int u = 0; u < kUnroll; ++u) v[u] = load16(r, off + (uint32_t)u * stride);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
-  // One word per block keeps the loads alive; the value itself is meaningless.
-  __shared__ uint32_t red[256];
-  red[threadIdx.x] = acc;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t a = 0;
-    for (int i = 0; i < 256; ++i) a ^= red[i];
-    sink[blockIdx.x] = a;
+  for (; off < bytes; off += stride) {
+    const u32x4 v = load16(r, off);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
   }
+  if (acc == kSentinel) sink[blockIdx.x] = acc;
 }
 
 }  // namespace

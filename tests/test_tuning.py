@@ -191,24 +191,32 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
         if tuning.row_bucket(rows) == rows:
             assert planner in cands
     gemv = [c for c in cands if c.kernel == "gemv"]
-    # GEMV plans exist for up to 4 rows: 2 and 4 columns per workgroup, and for each number of
+    # GEMV plans exist for up to 4 rows: 2, 4 and 8 columns per group, and for each number of
     # passes over K's 16-byte chunks the fewest waves (of 64 lanes) that make it; with more
     # than one pass, at most 8 of projections x columns x rows (registers)
     bucket = tuning.row_bucket(rows)
     chunks = k * bits // 128
 
-    def groups(w):  # column groups per workgroup: one pass over K in whole rows of 16 lanes
+    def groups(w):  # column groups per workgroup
+        if chunks <= 64:  # whole groups in every wave
+            return w * (64 // chunks if chunks % 16 == 0 else 1)
         return 64 * w // chunks if chunks <= 64 * w and chunks % 16 == 0 else 1
 
-    waves = {-(-chunks // (64 * p)) for p in range(1, 17)} & set(range(1, 9))
-    waves |= {w for w in range(1, 9) if groups(w) >= 2 and 64 * w % chunks == 0}
+    if chunks <= 64:
+        waves = set(range(1, 9))
+    else:
+        waves = {-(-chunks // (64 * p)) for p in range(1, 17)} & set(range(1, 9))
+        waves |= {w for w in range(1, 9) if groups(w) >= 2 and 64 * w % chunks == 0}
 
     def fits(c, w):
-        return chunks <= 64 * w or nproj * c * min(bucket, 4) <= 8
+        one_pass = chunks <= 64 * w
+        if c == 8:  # eight columns: one projection of up to two rows, in one pass
+            return one_pass and nproj == 1 and bucket <= 2
+        return one_pass or nproj * c * min(bucket, 4) <= 8
 
     # ... each in both workgroup orders; a workgroup covers groups(w) groups of c columns
     assert sorted((c.strips, c.tiles, c.order) for c in gemv) == (
-        sorted((n // (c * groups(w)), w, o) for c in (2, 4) for w in waves for o in (0, 1)
+        sorted((n // (c * groups(w)), w, o) for c in (2, 4, 8) for w in waves for o in (0, 1)
                if fits(c, w) and n % (c * groups(w)) == 0)
         if bucket <= 4 else [])
     for c in cands:
@@ -260,8 +268,9 @@ def test_installed_plans_are_bucketed_per_dtype_and_size_the_workspace(clean_pla
     (QmvPlan("staged", 25, 280, 1), "ksplit must be in 1..K/64"),
     (QmvPlan("staged", 7, 280, 1), "equal-length splits"),  # 24 steps in 7 splits is 6 of 4
     (QmvPlan("gemv", 2, 2240, 4), "does not split K"),
-    (QmvPlan("gemv", 1, 1120, 1), "GEMV strips must be"),   # 8 columns per workgroup
-    (QmvPlan("gemv", 1, 1120, 4), "GEMV strips must be"),   # 4 waves: 5 groups of 48 chunks
+    (QmvPlan("gemv", 1, 1120, 1), "does not hold this many columns"),  # 8 columns, 2 proj
+    (QmvPlan("gemv", 1, 560, 1), "GEMV strips must be"),    # 16 columns per workgroup
+    (QmvPlan("gemv", 1, 1120, 5), "GEMV strips must be"),   # 5 waves: 5 groups of 48 chunks
     (QmvPlan("gemv", 1, 2240, 0), "in 1..8"),
     (QmvPlan("gemv", 1, 2240, 9), "in 1..8"),
     (QmvPlan("gemv", 1, 2240, 1, 2), "order must be 0 or 1"),
