@@ -461,10 +461,12 @@ def section_ceiling(mt, device, stream, args):
 
 def traffic_probe(mt, gen, device, args):
     """Eager launches for the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE, then
-    WRITE_SIZE): a plain 256 MiB device copy (the calibration kernel of known size), then the
-    headline SwiGLU and down kernels over the 28-layer stack (layouts and plans as benchmarked:
-    run with the decision cache of a tuned run and METILE_AMD_DISABLE_TUNING=1, so that no
-    candidate plan is measured here), three passes each."""
+    WRITE_SIZE): a plain 256 MiB device copy (the calibration kernel of known size), then three
+    passes of each measured kernel, with the layouts and plans of a tuned run (run with its
+    decision cache and METILE_AMD_DISABLE_TUNING=1, so that no candidate plan is measured here):
+    the headline SwiGLU and down kernels over the 28-layer stack at M = 1; config 0 and config 3
+    at M = 1 over four weight copies; the dense MLP of config 2 at M = 1 and M = 128; the
+    prefill GEMMs of config 4. Prints the dispatch order and each phase's layouts."""
     src = torch.empty(256 << 20, dtype=torch.uint8, device=device).fill_(3)
     dst = torch.empty_like(src)
     for _ in range(5):
@@ -483,15 +485,58 @@ def traffic_probe(mt, gen, device, args):
         for h, (_g, _u, d) in zip(hs, layers):
             mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
     torch.cuda.synchronize()
-    print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20, "layouts": layouts}),
+    del layers, native, packed
+    phases = [{"phase": "headline", "layouts": layouts}]
+    for name, k, n, bits in (("config0", HIDDEN, INTER, 4), ("config3", 5120, 17408, 8)):
+        ws_native = [make_affine(gen, device, k, n, bits) for _ in range(4)]
+        ws_packed = [repacked(mt, w, bits) for w in ws_native]
+        xv = torch.randn(1, k, generator=gen, device=device).to(torch.bfloat16)
+        layout = choose_layout(args, xv, ws_native[0], ws_packed[0], bits)
+        for _ in range(3):
+            for w in (ws_packed if layout == "repacked" else ws_native):
+                mt.affine_qmv(xv, *w, group_size=GROUP, bits=bits)
+        torch.cuda.synchronize()
+        phases.append({"phase": name, "layout": layout})
+        del ws_native, ws_packed
+    h, i = 2048, 8192
+    dense = [tuple((torch.randn(nn, kk, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+                   for nn, kk in ((i, h), (i, h), (h, i))) for _ in range(4)]
+    for m in (1, 128):
+        xv = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
+        rv = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
+        for _ in range(3):
+            for g, u, d in dense:
+                mt.dense_qmv(mt.dense_swiglu(xv, g, u), d, rv)
+        torch.cuda.synchronize()
+        phases.append({"phase": f"config2_m{m}"})
+    del dense
+    for k, n in ((HIDDEN, INTER), (INTER, HIDDEN)):
+        ws = [make_affine(gen, device, k, n) for _ in range(4)]
+        xv = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
+        if not args.no_tune:
+            from metile_amd import tuning
+
+            tuning.ensure_gemm_plan(xv, *ws[0], group_size=GROUP)
+        for _ in range(3):
+            for w in ws:
+                mt.affine_matmul(xv, *w, group_size=GROUP, bits=BITS)
+        torch.cuda.synchronize()
+        phases.append({"phase": f"config4_{k}x{n}"})
+        del ws
+    print(json.dumps({"traffic_probe": "done", "copy_bytes": 256 << 20, "phases": phases}),
           flush=True)
 
 
-def prefill_probe(mt, gen, device):
-    """Eager launches for the prefill GEMM counter runs: three of each config-4 projection."""
+def prefill_probe(mt, gen, device, args):
+    """Eager launches for the prefill GEMM counter runs: three of each config-4 projection, with
+    the plan of a tuned run when its decision cache is given (METILE_AMD_DISABLE_TUNING=1)."""
     for k, n in ((HIDDEN, INTER), (INTER, HIDDEN)):
         w = make_affine(gen, device, k, n)
         x = torch.randn(512, k, generator=gen, device=device).to(torch.bfloat16)
+        if not args.no_tune:
+            from metile_amd import tuning
+
+            tuning.ensure_gemm_plan(x, *w, group_size=GROUP)
         for _ in range(3):
             mt.affine_matmul(x, *w, group_size=GROUP, bits=BITS)
         torch.cuda.synchronize()
@@ -649,7 +694,7 @@ def main():
         traffic_probe(mt, gen, device, args)
         return
     if args.prefill_probe:
-        prefill_probe(mt, gen, device)
+        prefill_probe(mt, gen, device, args)
         return
 
     with torch.cuda.stream(stream):
