@@ -30,6 +30,8 @@ as many replays timed one by one. The JSON line (kept under 8 KB) also carries:
 * ``ceiling``: measured streaming ceilings: one launch of ``mt_stream_read`` at each byte count,
   the step's own structure (two dependent launches per layer over 28 layers) and the launch
   floor of a dependent graph launch;
+* ``host_overhead_m1``: the host cost of one eager MLP call at M=1 at each caller level (C ABI,
+  torch operator, executor, patched transformers module), beside its GPU time;
 * ``cpu_baseline``: the NumPy oracle on this host's cores (variant B: weights dequantized ahead
   of time; variant A: unpack every call), with the host's CPU model and core count.
 
@@ -322,6 +324,68 @@ def section_mlp(mt, gen, device, stream, args):
                 timed(native_stack, stream, steps, args.warmup, LAYERS).mean, 3)
     del layers, native
     return rows_out, kernel, step
+
+
+def section_host(mt, gen, device, stream, args):
+    """Host cost of one eager MLP call at M=1 (Qwen2.5-1.5B MLP, int4, group 64), the price the
+    model-level caller pays per decoder layer and token when it does not replay a graph. For each
+    caller level: ``host_us``, the mean time to issue one call (200 back-to-back calls, no
+    synchronisation inside), and ``wall_us``, the mean time per call until the last result is
+    ready. Levels: the bare C-ABI call with prepared pointers (``mt_affine_mlp``); the torch
+    operator (``affine_mlp``: guards, workspace lookup, ctypes); the bound executor
+    (``mlx_affine_mlp_executor``); a transformers ``Qwen2MLP`` quantized by ``quantize_mlp``
+    under ``patch_quantized_mlp`` (tuned SwiGLU, then the module's down projection); and the same
+    module's residual-fused MLP as ``patch_graph_fusion`` runs it. When ``host_us`` exceeds the
+    GPU time of a call (``rows_us`` at M=1), eager decode is bound by the host."""
+    from metile_amd import _lib
+    from metile_amd import model as MM
+    from metile_amd import quantized as Q
+
+    (g, u, d) = make_layer(gen, device)
+    x = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    res = torch.randn(1, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+    lib = _lib.lib()
+    y = torch.empty(1, HIDDEN, dtype=torch.bfloat16, device=device)
+    ws = Q.workspace(device, lib.mt_affine_mlp_workspace_bytes(1, HIDDEN, INTER, GROUP, BITS))
+    cargs = (x.data_ptr(), *[t.data_ptr() for t in (*g, *u, *d)], res.data_ptr(), y.data_ptr(),
+             1, HIDDEN, INTER, GROUP, BITS, _lib.MT_BF16, ws.data_ptr(), ws.numel(),
+             torch.cuda.current_stream(device).cuda_stream)
+    ex = mt.mlx_affine_mlp_executor(x, *g, *u, *d, res)
+    levels = [("capi", lambda: lib.mt_affine_mlp(*cargs)),
+              ("affine_mlp", lambda: mt.affine_mlp(x, g, u, d, residual=res)),
+              ("executor", lambda: ex(x, res))]
+    try:
+        from transformers import Qwen2Config
+        from transformers.models.qwen2.modeling_qwen2 import Qwen2MLP
+
+        mlp = Qwen2MLP(Qwen2Config(hidden_size=HIDDEN, intermediate_size=INTER,
+                                   hidden_act="silu")).to(device=device, dtype=torch.bfloat16)
+        holder = torch.nn.Module()
+        holder.layers = torch.nn.ModuleList([torch.nn.Module()])
+        holder.layers[0].mlp = mlp
+        MM.quantize_mlp(holder)
+        replacements = MM.patch_quantized_mlp(holder)
+        levels += [("patched_mlp_module", lambda: mlp(x)),
+                   ("fused_residual_module", lambda: MM._execute_quantized_mlp(mlp, x, res))]
+    except ImportError:
+        replacements = []
+    out = {}
+    calls = 200
+    with torch.no_grad():
+        for name, fn in levels:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(calls):
+                fn()
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            out[name] = {"host_us": round((t1 - t0) / calls * 1e6, 2),
+                         "wall_us": round((t2 - t0) / calls * 1e6, 2)}
+    MM.restore_patches(replacements)
+    return out
 
 
 def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
@@ -699,6 +763,7 @@ def main():
 
     with torch.cuda.stream(stream):
         rows_out, kernel, step = section_mlp(mt, gen, device, stream, args)
+        host = section_host(mt, gen, device, stream, args)
         configs, ceiling = {}, None
         if not args.headline_only:
             configs["0"] = section_qmv(mt, gen, device, stream, args, HIDDEN, INTER, 4, ROWS)
@@ -758,6 +823,7 @@ def main():
                                    for m, r in rows_out.items()},
         "roofline": roofline,
         "native_layout_us": kernel["native_layout_us"],
+        "host_overhead_m1": host,
     }
     if ceiling:
         result["ceiling"] = ceiling

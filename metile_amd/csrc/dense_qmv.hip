@@ -49,8 +49,15 @@ __device__ __forceinline__ uint16_t typed_swiglu(float g, float u) {
   return f32_to_act<DT>(act * right);
 }
 
+// Workgroups per CU the kernel is built for: two for up to 64 rows; one for 128-row tiles, whose
+// accumulators (4 row tiles x NPROJ) leave room for a deep register ring only with the CU's
+// whole register file.
+template <int MT>
+constexpr int dense_occupancy() { return MT >= 4 ? 1 : 2; }
+
 template <int DT, int MT, int NPROJ, int STAGES>
-__global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParams args) {
+__global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_kernel(
+    const DenseParams args) {
   const DenseParams p = preload_args(args);  // all arguments in one batch of scalar loads
   __shared__ float red[kWaves][NPROJ][32][33];
   __shared__ int last_flag;
@@ -84,23 +91,31 @@ __global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParam
   }
 
   DStage<NPROJ, MT> ring[STAGES];
+  // Out-of-range offsets are set with oob_unless (x_row of a row past M already is), not
+  // with selects: with selects the compiler could no longer count the ring's loads and waited
+  // for nearly all of them before every step.
   auto load_stage = [&](DStage<NPROJ, MT>& S, int st) {
     const bool ok = st < w_end;
     const uint32_t woff = w_row + (uint32_t)st * 128u;
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], ok ? woff + 16u * e : kOOB);
+      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], oob_unless(ok, woff + 16u * e));
 #pragma unroll
     for (int rt = 0; rt < MT; ++rt) {
-      const bool xok = ok && x_row[rt] != kOOB;
       const uint32_t xoff = x_row[rt] + (uint32_t)st * 128u;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S.x[rt][e] = load16(rx, xok ? xoff + 16u * e : kOOB);
+      for (int e = 0; e < 4; ++e) S.x[rt][e] = load16(rx, oob_unless(ok, xoff + 16u * e));
     }
   };
+  // The ring is filled in stage order: the scheduler may not issue a later stage's loads
+  // first, or the first step would wait for all of them (and the loop, whose wait counts also
+  // cover its entry, for nearly every load in flight).
 #pragma unroll
-  for (int d = 0; d < STAGES; ++d) load_stage(ring[d], w_beg + d);
+  for (int d = 0; d < STAGES; ++d) {
+    load_stage(ring[d], w_beg + d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
   f32x16 acc[NPROJ][MT];
 #pragma unroll
@@ -194,11 +209,17 @@ __global__ __launch_bounds__(kThreads, 2) void dense_qmv_kernel(const DenseParam
     __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Register ring depth: the stages that fit beside the accumulators in the registers of one
+// wave (256 at two workgroups per CU, 512 at one), with at most 60 loads in flight: the
+// hardware counts at most 63 outstanding loads per wave, and a ring deeper than that count
+// makes the compiler wait for almost every load before each step.
 template <int NPROJ, int MT>
 constexpr int dense_stages() {
   constexpr int per_stage = 16 * NPROJ + 16 * MT;
-  constexpr int s = 112 / per_stage;
-  return s < 1 ? 1 : s;
+  constexpr int loads = 4 * NPROJ + 4 * MT;
+  constexpr int budget = dense_occupancy<MT>() == 1 ? 448 - 16 * NPROJ * MT : 112;
+  constexpr int s = budget / per_stage < 60 / loads ? budget / per_stage : 60 / loads;
+  return s < 1 ? 1 : (s > 4 ? 4 : s);
 }
 
 template <int DT, int NPROJ>
