@@ -152,14 +152,20 @@ _quantized_mlp_executor_cache: dict[int, tuple] = {}
 
 
 def _execute_quantized_mlp(module, values, residual=None):
-    """Without a residual: the fused gate/up SwiGLU kernel on the shape's tuned plan, over the
-    code layout (MLX rows or repacked, both held by ``QuantizedLinear``) that plan reads fastest
-    (the reference calls its tuned ``mlx_affine_swiglu`` here), then the module's down projection.
-    With one: ``down(swiglu(values)) + residual`` through an MLP executor bound to this module's
-    repacked codes, created (tuned, fidelity-gated) on first use and cached while the module
-    lives (``metile/integrations/mlx_lm.py:3837-3886``)."""
-    gate, up = module.gate_proj, module.up_proj
-    if residual is None:
+    """``down(swiglu(values)) (+ residual)`` through an MLP executor bound to this module's
+    weights in both code layouts: created (tuned per row bucket, fidelity-gated) on first use and
+    cached while the module lives (``metile/integrations/mlx_lm.py:3837-3886``); each call is one
+    C-ABI call over pre-validated weights (``BoundMlp``). Without a residual this is the
+    reference's tuned SwiGLU followed by the module's down projection: the hidden activation is
+    rounded to the activation type between the two, as there. Prefill-sized calls (at least
+    ``PREFILL_ROWS`` rows), and modules whose down projection is not an affine
+    ``QuantizedLinear`` of the same format, run the SwiGLU kernel and then the module's down
+    projection (the prefill GEMM at those rows)."""
+    gate, up, down = module.gate_proj, module.up_proj, module.down_proj
+    rows = values.numel() // values.shape[-1]
+    down_ok = (isinstance(down, QuantizedLinear) and down.mode == "affine"
+               and down.group_size == gate.group_size and down.bits == gate.bits)
+    if residual is None and (rows >= PREFILL_ROWS or not down_ok):
         layouts = {"repacked": (gate.packed, gate.scales, gate.biases,
                                 up.packed, up.scales, up.biases),
                    "mlx": (gate.weight, gate.scales, gate.biases,
@@ -172,7 +178,6 @@ def _execute_quantized_mlp(module, values, residual=None):
     key = id(module)
     cached = _quantized_mlp_executor_cache.get(key)
     if cached is None or cached[0]() is not module:
-        down = module.down_proj
         executor = bind_mlp_executor(
             values,
             ((gate.weight, gate.scales, gate.biases), (up.weight, up.scales, up.biases),

@@ -38,15 +38,23 @@ _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_handle(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle (torch's raw getter when it has
+    one: it builds no Stream object, about a microsecond less per call)."""
+    if _raw_stream is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
     return torch.cuda.current_stream(device).cuda_stream
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, nbytes: int, stream: int | None = None) -> torch.Tensor:
     """Return a zero-initialised uint8 workspace of at least ``nbytes`` for the current stream.
 
     Calls on one stream are ordered, so they may share it; the kernels leave its counter
-    region zeroed after each call. A buffer that is outgrown is kept, not freed, so that graphs
+    region zeroed after each call. ``stream``: the current stream's handle, if the caller has it. A buffer that is outgrown is kept, not freed, so that graphs
     captured over it stay valid.
 
     A buffer is never created or grown during graph capture: its zero fill would only be
@@ -54,7 +62,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     uninitialised. Run the call once on the capturing stream, outside capture, first.
     """
     key = (device.index if device.index is not None else torch.cuda.current_device(),
-           _stream_handle(device))
+           _stream_handle(device) if stream is None else stream)
     with _ws_lock:
         buf = _workspaces.get(key)
         if buf is None or buf.numel() < nbytes:
@@ -254,6 +262,87 @@ def affine_mlp(values, gate, up, down, *, group_size=64, bits=4, residual=None):
     else:
         _lib.check(L.mt_affine_mlp_layouts(*args, _layout_code(gw), _layout_code(dw), *tail))
     return out
+
+
+class BoundMlp:
+    """``affine_mlp`` over fixed weights, for callers that run the same MLP on every token (the
+    executors and the model-level caller). The weights are validated and their device pointers
+    taken once; a call checks only the activations and the residual, takes a workspace and makes
+    the one C-ABI call, which keeps the host cost of an eager decode step near the C ABI's own.
+    Results are those of ``affine_mlp`` over the same triples, bit for bit (the same entry
+    point). Inputs it does not take (another dtype, width or device) go through ``affine_mlp``,
+    which raises the reference's errors."""
+
+    __slots__ = ("triples", "group_size", "bits", "hdim", "idim", "dtype", "device", "code",
+                 "wptrs", "layouts", "need", "keep")
+
+    def __init__(self, gate, up, down, *, group_size=64, bits=4):
+        gw, gs, gb = gate
+        uw, us, ub = up
+        dw, ds, db = down
+        if _repacked(gw) != _repacked(uw):
+            raise ValueError("affine MLP gate and up weights must share one code layout")
+        _require_device(gw, gs, gb, uw, us, ub, dw, ds, db)
+        self.code = _dtype_code(gs.dtype)
+        self.idim, self.hdim = _code_shape(gw, bits)
+        probe = torch.empty(1, self.hdim, dtype=gs.dtype, device="meta")
+        _check_params(probe, gw, gs, gb, group_size, bits, "affine MLP gate")
+        _check_params(probe, uw, us, ub, group_size, bits, "affine MLP up")
+        if (_code_shape(dw, bits) != (self.hdim, self.idim)
+                or tuple(ds.shape) != (self.hdim, self.idim // group_size)
+                or tuple(db.shape) != tuple(ds.shape) or ds.dtype != gs.dtype
+                or db.dtype != gs.dtype or us.dtype != gs.dtype or gb.dtype != gs.dtype):
+            raise ValueError("affine MLP received incompatible down-projection parameters")
+        self.triples = (gate, up, down)
+        self.group_size, self.bits = group_size, bits
+        self.dtype, self.device = gs.dtype, gs.device
+        self.keep = [_as_u32(gw), gs.contiguous(), gb.contiguous(), _as_u32(uw), us.contiguous(),
+                     ub.contiguous(), _as_u32(dw), ds.contiguous(), db.contiguous()]
+        self.wptrs = tuple(t.data_ptr() for t in self.keep)
+        self.layouts = (_layout_code(gw), _layout_code(dw))
+        self.need = {}
+
+    def _general(self, values, residual):
+        return affine_mlp(values, *self.triples, group_size=self.group_size, bits=self.bits,
+                          residual=residual)
+
+    def __call__(self, values, residual=None):
+        if (values.dtype != self.dtype or values.device != self.device
+                or values.shape[-1] != self.hdim):
+            return self._general(values, residual)
+        lead = values.shape[:-1]
+        x = values.reshape(-1, self.hdim)
+        if not x.is_contiguous():
+            x = x.contiguous()
+        m = x.shape[0]
+        out = torch.empty(*lead, self.hdim, dtype=self.dtype, device=self.device)
+        if m == 0:
+            return out
+        rptr = None
+        if residual is not None:
+            if (residual.shape != out.shape or residual.dtype != self.dtype
+                    or residual.device != self.device):
+                return self._general(values, residual)
+            r = residual.reshape(m, self.hdim)
+            if not r.is_contiguous():
+                r = r.contiguous()
+            rptr = r.data_ptr()
+        L = _lib.lib()
+        stream = _stream_handle(self.device)
+        for attempt in (0, 1):
+            need = self.need.get(m) if attempt == 0 else None
+            if need is None:  # installed plans may change the need: refreshed on a refusal
+                need = self.need[m] = L.mt_affine_mlp_workspace_bytes(
+                    m, self.hdim, self.idim, self.group_size, self.bits)
+            ws = workspace(self.device, need, stream)
+            st = L.mt_affine_mlp_layouts(
+                x.data_ptr(), *self.wptrs, rptr, out.data_ptr(), m, self.hdim, self.idim,
+                self.group_size, self.bits, self.code, *self.layouts, ws.data_ptr(), ws.numel(),
+                stream)
+            if st != _lib.MT_ERR_WORKSPACE:
+                break
+        _lib.check(st)
+        return out
 
 
 def affine_dequantize(weight, scales, biases, *, group_size=64, bits=4):
@@ -561,9 +650,11 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
         (down_weight, down_scales, down_biases) = mlx
     chosen = {}  # row bucket -> (gate, up, down) in the layouts picked for it
 
+    chunk = 16 if group_size == 32 else 32  # rows of one dispatch
+
     def bucket(values):
         rows = values.numel() // values.shape[-1]
-        return _tuning.row_bucket(_tuning.dispatch_rows(max(rows, 1), group_size)[0])
+        return _tuning.row_bucket(min(max(rows, 1), chunk))
 
     def stages(values):
         key = bucket(values)
@@ -601,10 +692,16 @@ def bind_mlp_executor(sample_values, mlx, packed, sample_residual, *, group_size
                                    sample_residual, group_size=group_size, bits=bits),
         "affine residual QMV")
 
+    bound = {}  # row bucket -> BoundMlp over the layouts decided for it
+
     def execute(values, residual):
-        gate, up, down = stages(values)
-        return affine_mlp(values, gate, up, down, group_size=group_size, bits=bits,
-                          residual=residual)
+        key = bucket(values)
+        call = bound.get(key)
+        if call is None:
+            call = BoundMlp(*stages(values), group_size=group_size, bits=bits)
+            if key in chosen or not autotune:  # final: decided (or never tuned)
+                bound[key] = call
+        return call(values, residual)
 
     return execute
 

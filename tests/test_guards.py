@@ -202,3 +202,18 @@ def test_dequantize_validates_scale_and_code_shapes():
         mt.affine_dequantize(w, s, b, bits=3)
     with pytest.raises(ValueError, match="ROCm device tensors"):
         mt.affine_dequantize(w, s, b)  # valid shapes, host tensors
+
+
+def test_bound_mlp_checks_its_weights_once_on_the_host():
+    """``BoundMlp`` runs the MLP's weight checks at construction (no device work)."""
+    import torch
+
+    from metile_amd.quantized import BoundMlp
+
+    h, i = 128, 256
+    w = torch.zeros(i, h // 8, dtype=torch.int32)
+    s = torch.zeros(i, h // 64, dtype=torch.bfloat16)
+    dw = torch.zeros(h, i // 8, dtype=torch.int32)
+    ds = torch.zeros(h, i // 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        BoundMlp((w, s, s), (w, s, s), (dw, ds, ds))
