@@ -57,7 +57,8 @@ constexpr int kSbRowWords = kMaxGroupsPerSplit / 2 + 2;
 // Eight waves per strip ("tile"), one or two tiles per workgroup; the workgroup's activation
 // rows for its K range live in LDS, shared by its tiles.
 constexpr int kQmvLdsWaves = 8;
-constexpr int kQmvLdsMaxRows = 16;
+constexpr int kQmvLdsMaxRows = 32;        // groups of 64 or more
+constexpr int kQmvLdsMaxRowsHalf = 16;    // groups of 32 (two MFMA chains per step)
 // Dynamic LDS bound of one workgroup: two one-tile workgroups share a CU's 160 KiB, a two-tile
 // workgroup has the CU to itself (less room for the kernel's static shared variables).
 __host__ __device__ constexpr uint32_t qmv_lds_max_bytes(int tiles) {
@@ -67,7 +68,7 @@ __host__ __device__ constexpr uint32_t qmv_lds_max_bytes(int tiles) {
 // 16-byte activation chunks each thread stages (M * steps_per_split * 8 chunks in all, over
 // 512 * tiles threads).
 __host__ __device__ constexpr int qmv_lds_chunk_iters(int mrows, int tiles) {
-  return ((mrows <= 8 ? 5 : 8) + tiles - 1) / tiles;
+  return ((mrows <= 8 ? 5 : mrows <= 16 ? 8 : 12) + tiles - 1) / tiles;
 }
 
 // Dynamic LDS of one workgroup, byte offsets: scales and biases [tiles][2 nproj][32]

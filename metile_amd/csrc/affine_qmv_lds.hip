@@ -104,12 +104,20 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
 
   // ---- the residual this thread's output (row tid / 32, column tid % 32) adds, requested now
   // so that the workgroup finishing the strip does not wait for it at the end --------------
-  static_assert(MROWS * 32 <= kTileThreads, "one output per thread in the epilogue");
-  uint16_t res_pre = 0;
+  // Outputs per thread in the epilogue (output o = ttid + kTileThreads r): one up to 16 rows,
+  // two at 32.
+  constexpr int kResPer = (MROWS * 32 + kTileThreads - 1) / kTileThreads;
+  uint16_t res_pre[kResPer];
+#pragma unroll
+  for (int r = 0; r < kResPer; ++r) res_pre[r] = 0;
   if constexpr (NPROJ == 1) {
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.residual, p.residual ? (uint32_t)M * N * 2u : 0u);
-    const int ri = ttid >> 5, rc = ttid & 31;
-    res_pre = load2(rr, (ri < M && rc < width) ? ((uint32_t)ri * N + col0 + rc) * 2u : kOOB);
+#pragma unroll
+    for (int r = 0; r < kResPer; ++r) {
+      const int o = ttid + kTileThreads * r;
+      const int ri = o >> 5, rc = o & 31;
+      res_pre[r] = load2(rr, oob_unless(ri < M && rc < width, ((uint32_t)ri * N + col0 + rc) * 2u));
+    }
   }
 
   // ---- activation chunks: chunk c = row * cpr + cc holds elements [8 cc, 8 cc + 8) --------
@@ -287,7 +295,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
       out = silu_mul(v[0], v[1]);
     } else {
       out = v[0];
-      if (p.residual) out += act_to_f32<DT>(res_pre);  // output i * 32 + c is this thread's
+      // output i * 32 + c is this thread's output (i * 32 + c - ttid) / kTileThreads
+      if (p.residual) out += act_to_f32<DT>(res_pre[(i * 32 + c - ttid) / kTileThreads]);
     }
     p.y[oi] = f32_to_act<DT>(out);
   };
@@ -385,6 +394,9 @@ template <int BITS, int DT, int MROWS, int NPROJ, bool HALF, int TILES>
 hipError_t launch_lds_tiles(const QmvParams& p, hipStream_t stream) {
   if constexpr (HALF) {
     return launch_lds_stages<BITS, DT, MROWS, NPROJ, BITS == 4 ? 3 : 2, HALF, TILES>(p, stream);
+  } else if constexpr (MROWS == 32 && NPROJ == 2) {
+    // 32 rows of gate and up accumulators: a shallower ring keeps within 128 registers.
+    return launch_lds_stages<BITS, DT, MROWS, NPROJ, BITS == 4 ? 3 : 2, HALF, TILES>(p, stream);
   } else if constexpr (BITS == 8) {
     return launch_lds_stages<BITS, DT, MROWS, NPROJ, NPROJ == 2 ? 3 : 4, HALF, TILES>(p, stream);
   } else {
@@ -403,8 +415,10 @@ hipError_t launch_lds_rows(const QmvParams& p, hipStream_t stream) {
 
 template <int BITS, int DT, int NPROJ, bool HALF>
 hipError_t launch_lds_half(const QmvParams& p, hipStream_t stream) {
-  return p.M <= 8 ? launch_lds_rows<BITS, DT, 8, NPROJ, HALF>(p, stream)
-                  : launch_lds_rows<BITS, DT, 16, NPROJ, HALF>(p, stream);
+  if (p.M <= 8) return launch_lds_rows<BITS, DT, 8, NPROJ, HALF>(p, stream);
+  if (p.M <= 16 || HALF) return launch_lds_rows<BITS, DT, 16, NPROJ, HALF>(p, stream);
+  if constexpr (!HALF) return launch_lds_rows<BITS, DT, 32, NPROJ, HALF>(p, stream);
+  return hipErrorInvalidValue;
 }
 
 template <int BITS, int DT, int NPROJ>
@@ -422,8 +436,10 @@ hipError_t launch_lds_bits_dt(const QmvParams& p, int nproj, hipStream_t stream)
 }  // namespace
 
 bool affine_qmv_lds_fits(int M, int steps_per_split, int nproj, int group_size, int tiles) {
-  if (M < 1 || M > kQmvLdsMaxRows || (tiles != 1 && tiles != 2)) return false;
-  const int mrows = M <= 8 ? 8 : 16;
+  if (M < 1 || M > (group_size == 32 ? kQmvLdsMaxRowsHalf : kQmvLdsMaxRows) ||
+      (tiles != 1 && tiles != 2))
+    return false;
+  const int mrows = M <= 8 ? 8 : M <= 16 ? 16 : 32;
   if (M * steps_per_split * 8 > qmv_lds_chunk_iters(mrows, tiles) * kQmvLdsWaves * 64 * tiles)
     return false;
   // Groups staged per split (one more may straddle) within the scale rows.

@@ -175,7 +175,13 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
       if ((c.steps_per_split + mt::kQmvLdsWaves - 1) / mt::kQmvLdsWaves <= ring) break;
     }
   }
-  if (!use_lds_path(rows, plan.steps_per_split, nproj, group_size)) return plan;
+  // Up to 32 rows the staged kernel takes the call when its staging fits one workgroup of one
+  // strip, or (more rows over a long split) of two strips, which has the CU's LDS to itself.
+  const bool one_tile = use_lds_path(rows, plan.steps_per_split, nproj, group_size);
+  if (!one_tile &&
+      !(plan.strips % 2 == 0 &&
+        mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 2)))
+    return plan;
   plan.kernel = MT_QMV_STAGED;
   const long base = N / 32, ks = plan.ksplit;
   const long per_cu_base = (base * ks + kCus - 1) / kCus;  // workgroups on the busiest CU
@@ -198,7 +204,8 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
   // against 8.45 us). At fewer rows that staging is small and the 16-wave workgroup measured
   // slower (repacked SwiGLU at M = 1: 8.4 against 7.9 us).
   const long wgs = (long)plan.strips * plan.ksplit;
-  int tiles = (rows >= 4 && plan.strips % 2 == 0 && wgs > kCus && wgs <= 2L * kCus) ? 2 : 1;
+  int tiles = (!one_tile || (rows >= 4 && plan.strips % 2 == 0 && wgs > kCus &&
+                             wgs <= 2L * kCus)) ? 2 : 1;
   if (tiles == 2 && !mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 2))
     tiles = 1;
   plan.tiles = tiles;
@@ -207,7 +214,7 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
 
 // Rows per small-row dispatch: 32 (the register kernel's tile), 16 for groups of 32 (the
 // staged kernel's largest row bucket).
-int row_chunk(int group_size) { return group_size == 32 ? mt::kQmvLdsMaxRows : kRowChunk; }
+int row_chunk(int group_size) { return group_size == 32 ? mt::kQmvLdsMaxRowsHalf : kRowChunk; }
 
 // ---- installed plans -----------------------------------------------------------------------
 // A tuner measures the plans mt_affine_qmv_plan_candidates lists and installs the fastest for a
@@ -328,7 +335,8 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
       return "the register kernel runs N/32 strips, one per workgroup";
     return "";
   }
-  if (rows > mt::kQmvLdsMaxRows) return "more rows than the staged kernel takes";
+  if (rows > (group_size == 32 ? mt::kQmvLdsMaxRowsHalf : mt::kQmvLdsMaxRows))
+    return "more rows than the staged kernel takes";
   if (q.strips < base || q.strips > 2 * base || q.strips > kMaxStrips)
     return "staged strips must be in N/32..2N/32";
   if (q.tiles != 1 && q.tiles != 2) return "tiles must be 1 or 2";

@@ -226,7 +226,8 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
         elif c.kernel == "gemv":
             assert c.ksplit == 1 and c.workgroups == c.strips
         else:
-            assert rows <= 16 and n // 32 <= c.strips <= 2 * (n // 32) and c.strips % c.tiles == 0
+            assert rows <= (16 if g == 32 else 32)
+            assert n // 32 <= c.strips <= 2 * (n // 32) and c.strips % c.tiles == 0
         tuning.install_qmv_plan(rows, k, n, g, bits, nproj, torch.bfloat16, c)
         assert tuning.qmv_plan(rows, k, n, g, bits, nproj, torch.bfloat16) == c
 
@@ -287,10 +288,15 @@ def test_invalid_qmv_plans_are_rejected(plan, message, clean_plans):
 def test_plan_rules_that_depend_on_rows_and_groups(clean_plans):
     import torch
 
-    # the staged kernel takes at most 16 rows; the register kernel no groups of 32
-    with pytest.raises(ValueError, match="more rows than the staged kernel"):
+    # the staged kernel takes at most 32 rows (16 with groups of 32), within its LDS; the
+    # register kernel no groups of 32
+    with pytest.raises(ValueError, match="rows of one dispatch, at most 16"):
+        tuning.install_qmv_plan(17, 1024, 1536, 32, 4, 1, torch.bfloat16,
+                                QmvPlan("staged", 1, 48, 1))
+    with pytest.raises(ValueError, match="LDS does not hold"):
         tuning.install_qmv_plan(17, 1536, 8960, 64, 4, 1, torch.bfloat16,
                                 QmvPlan("staged", 1, 280, 1))
+    tuning.install_qmv_plan(17, 1536, 8960, 64, 4, 2, torch.bfloat16, QmvPlan("staged", 1, 280, 2))
     with pytest.raises(ValueError, match="groups of 64 or more"):
         tuning.install_qmv_plan(1, 1024, 1536, 32, 8, 1, torch.bfloat16,
                                 QmvPlan("register", 1, 48, 1))
