@@ -28,11 +28,14 @@ from .quantized import (
     affine_repack,
     affine_swiglu,
     mlx_affine_matmul,
+    mlx_affine_matmul_dispatches,
     mlx_affine_mlp_executor,
     mlx_affine_qmv,
     mlx_affine_qmv_nax,
     mlx_affine_residual_qmv,
+    mlx_affine_residual_qmv_dispatches,
     mlx_affine_swiglu,
+    mlx_affine_swiglu_dispatches,
     mlx_affine_swiglu_executor,
     mlx_affine_swiglu_qmv,
     mlx_affine_swiglu_qmv_nax,
@@ -66,11 +69,14 @@ __all__ = [
     "affine_repack",
     "affine_swiglu",
     "mlx_affine_matmul",
+    "mlx_affine_matmul_dispatches",
     "mlx_affine_mlp_executor",
     "mlx_affine_qmv",
     "mlx_affine_qmv_nax",
     "mlx_affine_residual_qmv",
+    "mlx_affine_residual_qmv_dispatches",
     "mlx_affine_swiglu",
+    "mlx_affine_swiglu_dispatches",
     "mlx_affine_swiglu_executor",
     "mlx_affine_swiglu_qmv",
     "mlx_affine_swiglu_qmv_nax",

@@ -512,6 +512,19 @@ def mlx_affine_swiglu(values, gate_weight, gate_scales, gate_biases, up_weight, 
                          up_biases, group_size=group_size, bits=bits)
 
 
+def mlx_affine_swiglu_dispatches():
+    """This process's SwiGLU dispatch decisions (``metile/backends/mlx_quantized.py:1835-1852``):
+    one dict per resolved dispatch shape with its plan, layout and source
+    (``metile_amd.tuning.dispatches``)."""
+    return _tuning.dispatches("swiglu")
+
+
+def mlx_affine_residual_qmv_dispatches():
+    """This process's one-projection (residual) QMV dispatch decisions
+    (``metile/backends/mlx_quantized.py:1627-1642``; ``metile_amd.tuning.dispatches``)."""
+    return _tuning.dispatches("qmv")
+
+
 def mlx_affine_swiglu_qmv(values, gate_weight, gate_scales, gate_biases, up_weight, up_scales,
                           up_biases, *, group_size=64, bits=4, block=32, outputs_per_simdgroup=1,
                           decode_dtype="f32"):
@@ -723,6 +736,12 @@ def mlx_affine_residual_qmv_guards(values, weight, scales, biases, residual, *, 
         raise ValueError("affine residual QMV parameters must match the input dtype")
     if tuple(residual.shape) != (*values.shape[:-1], n) or residual.dtype != values.dtype:
         raise ValueError("residual must match the affine QMV output shape and dtype")
+
+
+def mlx_affine_matmul_dispatches():
+    """This process's prefill GEMM dispatch decisions (``metile/backends/mlx_affine.py:409-422``;
+    ``metile_amd.tuning.dispatches``)."""
+    return _tuning.dispatches("matmul")
 
 
 def mlx_affine_matmul(values, weight, *, autotune=True):

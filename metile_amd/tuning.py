@@ -261,6 +261,7 @@ def clear_plans() -> None:
         _lib.check(_lib.lib().mt_plans_clear())
         _decided.clear()
         _decided_layouts.clear()
+        _resolved.clear()
 
 
 # ---- timing and ranking -------------------------------------------------------------------------
@@ -345,6 +346,10 @@ def choose(timings, baseline, cost, *, margin=SWITCH_MARGIN, tie=TIE_TOLERANCE):
 _lock = threading.RLock()
 _decided: dict[tuple, object] = {}
 _decided_layouts: dict[tuple, tuple] = {}
+# Every dispatch shape this process has resolved through ensure_qmv_plans, ensure_qmv_layout or
+# ensure_gemm_plan, with how: "measured" (tuned now), "cached" (a disk decision) or "planner"
+# (nothing decided: the library's own plan). Read by dispatches().
+_resolved: dict[tuple, str] = {}
 _identity: dict[int, dict] = {}
 _BASELINE = "planner"
 
@@ -608,11 +613,13 @@ def ensure_qmv_plans(values, weights, *, group_size, bits, autotune=True, retune
                 if (not autotune or not tuning_enabled()
                         or torch.cuda.is_current_stream_capturing()):
                     out[rows] = None
+                    _resolved.setdefault(mem, "planner")
                     continue  # not decided: the planner's plan, and measure another time
                 plan, record = _tune_qmv_dispatch(x[:rows], weights, group_size, bits, layout)
                 _write_decision(key, plan, {"op": "affine_qmv", **shape, **record})
             install_qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype, plan)
             _decided[mem] = plan
+            _resolved[mem] = "cached" if found else "measured"
             out[rows] = plan
     return out
 
@@ -662,6 +669,7 @@ def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retun
             decided = found and cached in names
             if decided:
                 chosen = cached
+                _resolved[mem] = "cached"
             elif autotune and tuning_enabled() and not torch.cuda.is_current_stream_capturing():
                 plan, code, record = _tune_qmv_layouts(
                     x[:rows], [(_LAYOUT_CODES[name], layouts[name]) for name in names],
@@ -670,6 +678,7 @@ def ensure_qmv_layout(values, layouts, *, group_size, bits, autotune=True, retun
                 _write_decision(key, plan, {"op": "affine_qmv_layout", **shape,
                                             "layouts": names, **record})
                 decided = True
+                _resolved[mem] = "measured"
             if decided:
                 install_qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype, plan)
                 _decided[mem] = plan
@@ -756,9 +765,56 @@ def ensure_gemm_plan(values, weight, scales, biases, *, group_size, autotune=Tru
         found, plan = (False, None) if retune else _read_decision(key, GemmPlan)
         if not found:
             if not autotune or not tuning_enabled() or torch.cuda.is_current_stream_capturing():
+                _resolved.setdefault(mem, "planner")
                 return None
             plan, record = _tune_gemm(x, weight, scales, biases, group_size)
             _write_decision(key, plan, {"op": "affine_matmul", **shape, **record})
         install_gemm_plan(rows, k, n, group_size, values.dtype, plan)
         _decided[mem] = plan
+        _resolved[mem] = "cached" if found else "measured"
         return plan
+
+
+def dispatches(op: str) -> tuple:
+    """This process's dispatch decisions for one operation, as the reference's
+    ``mlx_affine_swiglu_dispatches`` / ``mlx_affine_residual_qmv_dispatches`` /
+    ``mlx_affine_matmul_dispatches`` report theirs (``metile/backends/mlx_quantized.py:1627,1835``;
+    ``metile/backends/mlx_affine.py:409``): one dict per dispatch shape resolved so far, sorted
+    by shape. ``op`` is ``"swiglu"`` (two projections), ``"qmv"`` (one projection, with or
+    without a residual: the plan does not depend on it) or ``"matmul"`` (the prefill GEMM).
+
+    Each dict holds the shape (``rows`` is the row bucket the decision covers), the plan the
+    library runs for it now, the code layout when a layout decision picked one, and
+    ``source``: ``"measured"``, ``"cached"`` (from the decision cache on disk) or ``"planner"``
+    (nothing decided; the library's own plan)."""
+    if op not in ("swiglu", "qmv", "matmul"):
+        raise ValueError('op must be "swiglu", "qmv" or "matmul"')
+    with _lock:
+        resolved = dict(_resolved)
+        decided = dict(_decided)
+        layouts = dict(_decided_layouts)
+    out = []
+    for mem, source in resolved.items():
+        if op == "matmul":
+            if mem[0] != "gemm":
+                continue
+            _, device, bucket, k, n, group_size, dtype = mem
+            plan = decided.get(mem) or gemm_plan(bucket, k, n, group_size, dtype)
+            out.append({"rows": bucket, "input_features": k, "output_features": n,
+                        "dtype": str(dtype), "group_size": group_size, "bits": 4,
+                        "device": device, "tile": plan.tile, "ksplit": plan.ksplit,
+                        "source": source})
+            continue
+        if mem[0] != "qmv" or mem[7] != (2 if op == "swiglu" else 1):
+            continue
+        _, device, bucket, k, n, group_size, bits, nproj, dtype = mem
+        plan = decided.get(mem) or qmv_plan(bucket, k, n, group_size, bits, nproj, dtype)
+        layout = next((chosen for key, (_p, chosen) in layouts.items() if key[:9] == mem), None)
+        out.append({"rows": bucket, "input_features": k, "output_features": n,
+                    "dtype": str(dtype), "group_size": group_size, "bits": bits,
+                    "device": device, "kernel": plan.kernel, "ksplit": plan.ksplit,
+                    "strips": plan.strips, "tiles": plan.tiles, "order": plan.order,
+                    "layout": layout, "source": source})
+    out.sort(key=lambda d: (d["device"], d["input_features"], d["output_features"], d["dtype"],
+                            d["group_size"], d["bits"], d["rows"]))
+    return tuple(out)

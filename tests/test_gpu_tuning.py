@@ -165,12 +165,17 @@ def test_tuner_decides_persists_and_reloads(monkeypatch, tmp_path):
     installed = tuning.qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16)
     assert installed == (plan if plan is not None else planner)
     _check("tuned swiglu", torch_to_act(mt.mlx_affine_swiglu(xt, *gt, *ut), "bf16"), ref)
+    (seen,) = mt.mlx_affine_swiglu_dispatches()
+    assert (seen["rows"], seen["source"]) == (1, "measured")
+    assert tuning.QmvPlan(seen["kernel"], seen["ksplit"], seen["strips"], seen["tiles"],
+                          seen["order"]) == installed
 
     # a fresh process state: the decision comes back from the cache, no measuring
     tuning.clear_plans()
     monkeypatch.setenv("METILE_AMD_DISABLE_TUNING", "1")
     assert tuning.ensure_qmv_plans(xt, packed, group_size=64, bits=4) == decision
     assert tuning.qmv_plan(1, 1536, 8960, 64, 4, 2, torch.bfloat16) == installed
+    assert [d["source"] for d in mt.mlx_affine_swiglu_dispatches()] == ["cached"]
     # decisions apply to both code layouts: MLX codes give the same bits as repacked ones
     assert _same(mt.affine_swiglu(xt, *gt, *ut), mt.affine_swiglu(xt, *packed))
 
@@ -189,6 +194,8 @@ def test_layout_decision_persists_and_reloads(monkeypatch, tmp_path):
     layouts = {"repacked": packed, "mlx": mlx}
     layout = tuning.ensure_qmv_layout(ht, layouts, group_size=64, bits=4)
     assert layout in layouts
+    (seen,) = mt.mlx_affine_residual_qmv_dispatches()
+    assert (seen["rows"], seen["layout"], seen["source"]) == (1, layout, "measured")
     entries = tuning.load_decisions()
     assert len(entries) == 1
     record = next(iter(entries.values()))
@@ -231,6 +238,15 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     _check("tuned mlp, one row", torch_to_act(ex(xt[:1], rt[:1]), "bf16"), ref1, min_exact=0.85)
     rows = {(e["rows"], e["nproj"]) for e in tuning.load_decisions().values()}
     assert {(1, 1), (1, 2), (4, 1), (4, 2)} <= rows
+    # the executor's decisions, as the reference's dispatch introspection lists them
+    for seen, nproj in ((mt.mlx_affine_swiglu_dispatches(), 2),
+                        (mt.mlx_affine_residual_qmv_dispatches(), 1)):
+        assert {d["rows"] for d in seen} == {1, 4}
+        assert all(d["source"] == "measured" and d["layout"] in ("mlx", "repacked")
+                   for d in seen if d["rows"] == 4)
+        assert all(tuning.QmvPlan(d["kernel"], d["ksplit"], d["strips"], d["tiles"], d["order"])
+                   == tuning.qmv_plan(d["rows"], d["input_features"], d["output_features"], 64,
+                                      4, nproj, torch.bfloat16) for d in seen)
     # the prefill GEMM through the tuned reference entry
     w = affine_to_torch(O.make_affine_weight(1536, 1024, 4, 64, 9, 10), "bf16")
     aw = mt.AffineWeight.from_torch(*w)
@@ -240,5 +256,10 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     gemm = [e for e in tuning.load_decisions().values()
             if e["op"] == "affine_matmul"]
     assert len(gemm) == 1
+    (seen,) = mt.mlx_affine_matmul_dispatches()
+    assert (seen["rows"], seen["input_features"], seen["output_features"], seen["source"]) == (
+        256, 1024, 1536, "measured")
+    assert tuning.GemmPlan(seen["tile"], seen["ksplit"]) == tuning.gemm_plan(
+        200, 1024, 1536, 64, torch.bfloat16)
     print(f"[tuner gemm 200x1024x1536] planner {gemm[0]['planner']} {gemm[0]['planner_us']} us, "
           f"chosen {gemm[0]['plan']} {gemm[0]['chosen_us']} us", flush=True)

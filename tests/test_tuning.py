@@ -15,6 +15,7 @@ import multiprocessing
 import os
 
 import pytest
+import torch
 
 import metile_amd._lib as L
 from metile_amd import build, tuning
@@ -341,6 +342,47 @@ def test_gemm_plans(clean_plans):
     tuning.clear_plans()
     assert tuning.gemm_plan(m, k, n, 64, torch.bfloat16) == planner
     assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == before
+
+
+def test_dispatches_report_every_resolved_shape(clean_plans):
+    """The reference's ``*_dispatches()`` introspection (``mlx_quantized.py:1627,1835``,
+    ``mlx_affine.py:409``): one record per resolved shape, its plan as the library runs it
+    now (a decided plan, else the planner's), sorted by shape, cleared with the plans."""
+    import metile_amd as mt
+
+    bf = torch.bfloat16
+    swiglu = ("qmv", 0, 1, 1536, 8960, 64, 4, 2, bf)
+    down = ("qmv", 0, 16, 8960, 1536, 64, 4, 1, bf)
+    down1 = ("qmv", 0, 1, 8960, 1536, 64, 4, 1, bf)
+    gemm = ("gemm", 0, 512, 1536, 8960, 64, bf)
+    with tuning._lock:
+        tuning._resolved.update({swiglu: "measured", down: "planner", down1: "cached",
+                                 gemm: "cached"})
+        tuning._decided[swiglu] = QmvPlan("gemv", 1, 2240, 2, 1)
+        tuning._decided[down1] = QmvPlan("gemv", 1, 768, 5, 1)
+        tuning._decided_layouts[(*swiglu, ("repacked", "mlx"))] = (tuning._decided[swiglu],
+                                                                   "mlx")
+        tuning._decided[gemm] = GemmPlan(128, 1)
+
+    (sw,) = mt.mlx_affine_swiglu_dispatches()
+    assert sw == {"rows": 1, "input_features": 1536, "output_features": 8960,
+                  "dtype": "torch.bfloat16", "group_size": 64, "bits": 4, "device": 0,
+                  "kernel": "gemv", "ksplit": 1, "strips": 2240, "tiles": 2, "order": 1,
+                  "layout": "mlx", "source": "measured"}
+    qmv = mt.mlx_affine_residual_qmv_dispatches()
+    assert [(d["rows"], d["source"], d["layout"]) for d in qmv] == [(1, "cached", None),
+                                                                   (16, "planner", None)]
+    planner = tuning.qmv_plan(16, 8960, 1536, 64, 4, 1, bf)
+    assert (qmv[1]["kernel"], qmv[1]["ksplit"], qmv[1]["strips"], qmv[1]["tiles"]) == (
+        planner.kernel, planner.ksplit, planner.strips, planner.tiles)
+    assert qmv[0]["kernel"] == "gemv" and qmv[0]["strips"] == 768
+    (mm,) = mt.mlx_affine_matmul_dispatches()
+    assert (mm["rows"], mm["tile"], mm["ksplit"], mm["source"]) == (512, 128, 1, "cached")
+    with pytest.raises(ValueError, match="op must be"):
+        tuning.dispatches("dense")
+    tuning.clear_plans()
+    assert tuning.dispatches("swiglu") == tuning.dispatches("qmv") == () == \
+        tuning.dispatches("matmul")
 
 
 def test_candidate_buffer_contract():
