@@ -156,11 +156,19 @@ Plan planner_qmv(int rows, int K, int N, int nproj, int group_size, int bits) {
       c.ksplit = (steps + c.steps_per_split - 1) / c.steps_per_split;
       return c;
     };
-    if ((rows <= 8 || nproj == 1) &&
-        !mt::affine_qmv_lds_fits(rows, plan.steps_per_split, nproj, group_size, 1)) {
+    // A two-strip workgroup (the CU's LDS to itself) is taken before another K split: every
+    // split adds a partial-sum hand-off (one projection 1536 -> 8960 at M = 32: two strips
+    // unsplit 7.9 us against one strip over two splits 13.6 us; the down projection
+    // 8960 -> 1536 at M = 32: two strips over 6 splits 11.5 us against 9 splits 12.7 us).
+    auto staged_fits = [&](int steps_per_split) {
+      return mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size, 1) ||
+             (plan.strips % 2 == 0 &&
+              mt::affine_qmv_lds_fits(rows, steps_per_split, nproj, group_size, 2));
+    };
+    if ((rows <= 8 || nproj == 1) && !staged_fits(plan.steps_per_split)) {
       for (int ks = plan.ksplit + 1; ks <= 2 * plan.ksplit && ks <= steps; ++ks) {
         const Plan c = split_into(ks);
-        if (mt::affine_qmv_lds_fits(rows, c.steps_per_split, nproj, group_size, 1)) {
+        if (staged_fits(c.steps_per_split)) {
           plan = c;
           break;
         }

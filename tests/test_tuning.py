@@ -321,6 +321,12 @@ def test_plan_rules_that_depend_on_rows_and_groups(clean_plans):
     with pytest.raises(ValueError, match="too many groups per split"):
         tuning.install_qmv_plan(1, 8960, 1536, 64, 4, 1, torch.bfloat16,
                                 QmvPlan("register", 2, 48, 1))
+    # where one strip's staging does not fit, the planner takes two-strip workgroups before
+    # another K split (one projection at 32 rows: unsplit; the down projection: the fewest
+    # splits whose staging two strips hold, 6 of 24 steps each)
+    assert tuning.qmv_plan(32, 1536, 8960, 64, 4, 1, torch.bfloat16) == QmvPlan("staged", 1, 280, 2)
+    assert tuning.qmv_plan(32, 8960, 1536, 64, 4, 1, torch.bfloat16) == QmvPlan("staged", 6, 48, 2)
+    assert tuning.qmv_plan(16, 8960, 1536, 64, 4, 1, torch.bfloat16) == QmvPlan("staged", 5, 48, 1)
 
 
 def test_gemm_plans(clean_plans):
