@@ -487,7 +487,11 @@ def section_ceiling(mt, device, stream, args):
 
     def best(pairs, calls):
         top = None
-        for blocks in (1024, 2048, 4096):
+        # fixed grids (several batches per thread at large sizes), and grids that cover the
+        # largest buffer in one batch of 1, 2, 4 or 8 loads per thread
+        big = max(nbytes for _, nbytes in pairs)
+        sized = [min(65536, -(-big // (4096 * u))) for u in (1, 2, 4, 8)]
+        for blocks in dict.fromkeys([1024, 2048, 4096, *sized]):
             with torch.cuda.stream(stream):
                 run = reads(pairs, blocks)
                 run()
@@ -500,7 +504,7 @@ def section_ceiling(mt, device, stream, args):
 
     out = {}
     for label, nbytes in (("7.8MB", 7_765_504), ("15.5MB", 15_503_872), ("23.2MB", 23_269_376),
-                          ("100.7MB", 100_663_296)):
+                          ("94.7MB", 94_744_576), ("100.7MB", 100_663_296)):
         copies = copies_for(nbytes)
         bufs = [torch.ones(nbytes, dtype=torch.uint8, device=device) for _ in range(copies)]
         us, blocks = best([(b, nbytes) for b in bufs], copies)

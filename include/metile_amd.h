@@ -273,7 +273,8 @@ const char* mt_source_digest(void);
 /* ---- measurement -------------------------------------------------------------------------- */
 
 /* Reads `bytes` from `p` with `blocks` workgroups of 256 threads issuing 16-byte loads (grid
- * stride, 8 in flight per thread) and no reduction: the streaming-read ceiling of one launch.
+ * stride; per thread the fewest loads in flight, 1, 2, 4 or 8, that cover the buffer in one
+ * batch, else batches of 8) and no reduction: the streaming-read ceiling of one launch.
  * `sink` (at least `blocks` words) is written only when a thread's XOR of its data equals a
  * fixed sentinel, which keeps the loads alive. No counterpart entry point in the reference; it
  * is the analogue of its measured streaming-read constant (metile/target/agx.py:38). */

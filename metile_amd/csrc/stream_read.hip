@@ -8,30 +8,33 @@ namespace mt {
 
 namespace {
 
-constexpr int kUnroll = 8;
 constexpr uint32_t kSentinel = 0x9E3779B9u;
 
-// Grid-stride 16-byte loads: at each step the grid reads one contiguous span of
-// gridDim.x * 4 KiB (block b its 4 KiB at b * 4 KiB), up to kUnroll steps in flight per thread.
-// Each thread XOR-folds what it read and stores it only if it equals a sentinel, which keeps the
-// loads alive without a reduction at the end: the probe is the stream alone, with no tail a
-// reduction or store would add.
+// Grid-stride 16-byte loads, U per thread in flight: at each step the grid reads one contiguous
+// span of gridDim.x * 4 KiB (block b its 4 KiB at b * 4 KiB), U steps per batch. Only the last
+// batch can run past the end; its loads there take an out-of-range offset (bit 31 set; buffers
+// are below 2 GiB) and read zero. (A second batch requested before the first is folded measured
+// slower at every size.) The host picks U from the grid (the fewest loads per thread
+// that cover the buffer, at most 8), so a grid of bytes / (4 KiB * U) blocks issues all of its
+// loads in one batch, as a one-pass kernel does, with almost none out of range (those still
+// cost issue slots). Each thread XOR-folds what it read and stores it only if it equals a
+// sentinel, which keeps the loads alive without a reduction at the end: the probe is the stream
+// alone, with no tail a reduction or store would add.
+template <int U>
 __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* p, uint32_t bytes,
                                                           uint32_t* sink) {
   const __amdgpu_buffer_rsrc_t r = make_rsrc(p, bytes);
   const uint32_t stride = gridDim.x * 256u * 16u;
-  uint32_t off = (blockIdx.x * 256u + threadIdx.x) * 16u;
   uint32_t acc = 0;
-  for (; off + (kUnroll - 1) * stride < bytes; off += kUnroll * stride) {
-    u32x4 v[kUnroll];
+  for (uint32_t off = (blockIdx.x * 256u + threadIdx.x) * 16u; off < bytes; off += U * stride) {
+    u32x4 v[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) v[u] = load16(r, off + (uint32_t)u * stride);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t o = off + (uint32_t)u * stride;
+      v[u] = load16(r, oob_unless(o < bytes, o));
+    }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
-  }
-  for (; off < bytes; off += stride) {
-    const u32x4 v = load16(r, off);
-    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
   if (acc == kSentinel) sink[blockIdx.x] = acc;
 }
@@ -40,7 +43,13 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint8_t* p, uint
 
 hipError_t launch_stream_read(const void* p, uint32_t bytes, uint32_t* sink, int blocks,
                               hipStream_t stream) {
-  stream_read_kernel<<<blocks, 256, 0, stream>>>(static_cast<const uint8_t*>(p), bytes, sink);
+  const uint64_t span = (uint64_t)blocks * 256u * 16u;
+  const uint64_t steps = ((uint64_t)bytes + span - 1) / span;  // loads per thread
+  const uint8_t* b = static_cast<const uint8_t*>(p);
+  if (steps <= 1) stream_read_kernel<1><<<blocks, 256, 0, stream>>>(b, bytes, sink);
+  else if (steps <= 2) stream_read_kernel<2><<<blocks, 256, 0, stream>>>(b, bytes, sink);
+  else if (steps <= 4) stream_read_kernel<4><<<blocks, 256, 0, stream>>>(b, bytes, sink);
+  else stream_read_kernel<8><<<blocks, 256, 0, stream>>>(b, bytes, sink);
   return hipGetLastError();
 }
 

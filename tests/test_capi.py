@@ -80,3 +80,13 @@ def test_mlp_layouts_argument_checks_without_gpu():
     st = lib.mt_affine_mlp_layouts(*args, _lib.MT_LAYOUT_REPACKED, _lib.MT_LAYOUT_MLX, None, 0,
                                    None)
     assert st != 0 and "LAYOUT" not in lib.mt_last_error().decode()
+
+
+def test_stream_read_argument_checks_without_gpu():
+    lib = _lib.lib()
+    buf = ctypes.c_void_p(256)  # never dereferenced: every case fails validation first
+    for p, nbytes, sink, blocks in ((None, 4096, buf, 1), (buf, 0, buf, 1), (buf, 1 << 31, buf, 1),
+                                    (buf, 4096, None, 1), (buf, 4096, buf, 0),
+                                    (buf, 4096, buf, 65537)):
+        assert lib.mt_stream_read(p, nbytes, sink, blocks, None) == _lib.MT_ERR_INVALID_ARGUMENT
+        assert "below 2 GiB" in lib.mt_last_error().decode()
