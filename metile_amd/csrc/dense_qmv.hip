@@ -66,15 +66,27 @@ constexpr int dense_occupancy() { return MT >= 4 ? 1 : 2; }
 template <int MT>
 constexpr bool dense_x_lds() { return MT >= 2; }
 
+// LDS of one workgroup, 16-byte units: during the K loop each wave's staged activation tile
+// (XLDS) and weight tile ([NPROJ][32 columns][8 chunks], the same swizzle); after it the
+// cross-wave reduction buffer [kWaves][NPROJ][32][33] (fp32), in the same space.
+template <int MT, int NPROJ>
+constexpr int dense_lds_units() {
+  constexpr int per_wave = (dense_x_lds<MT>() ? MT * 32 * 8 : 0) + NPROJ * 32 * 8;
+  constexpr int loop = kWaves * per_wave;
+  constexpr int red = (kWaves * NPROJ * 32 * 33 + 3) / 4;
+  return loop > red ? loop : red;
+}
+
 template <int DT, int MT, int NPROJ, int STAGES>
 __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_kernel(
     const DenseParams args) {
   const DenseParams p = preload_args(args);  // all arguments in one batch of scalar loads
   constexpr bool XLDS = dense_x_lds<MT>();
-  __shared__ float red[kWaves][NPROJ][32][33];
+  constexpr int kXUnits = XLDS ? MT * 32 * 8 : 0;  // per wave
+  constexpr int kWUnits = NPROJ * 32 * 8;          // per wave
+  __shared__ __attribute__((aligned(16))) u32x4 smem[dense_lds_units<MT, NPROJ>()];
   __shared__ int last_flag;
-  // [wave][MT * 32 rows][8 chunks] of 16 bytes: one K step of the wave's activation tile
-  __shared__ __attribute__((aligned(16))) u32x4 xs[XLDS ? kWaves : 1][XLDS ? MT * 32 : 1][8];
+  auto red = reinterpret_cast<float (*)[NPROJ][32][33]>(smem);  // [kWaves][NPROJ][32][33]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -96,7 +108,13 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
   __amdgpu_buffer_rsrc_t rw[NPROJ];
 #pragma unroll
   for (int pr = 0; pr < NPROJ; ++pr) rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * row_bytes);
-  const uint32_t w_row = (uint32_t)(strip * 32 + j) * row_bytes + 64u * h;
+  // Weights are loaded 8 lanes per column like the staged activations: instruction e of a
+  // projection reads columns 8 e + lane / 8 of the strip, chunk lane % 8 of each step, and the
+  // wave reads them back from LDS as the MFMA B operand (column j, chunks 4 h + e).
+  const uint32_t w_row = (uint32_t)(strip * 32 + (lane >> 3)) * row_bytes + 16u * (lane & 7);
+  const uint32_t w_step8 = 8u * row_bytes;
+  u32x4* const xs = smem + wave * (kXUnits + kWUnits);  // [MT * 32 rows][8]
+  u32x4* const ws = xs + kXUnits;                        // [NPROJ][32 columns][8]
   // Direct operand loads: lane (j, h) reads row 32 rt + j, K [32 h, 32 h + 32) of each step.
   // Staged loads (XLDS): instruction e of row tile rt reads rows 32 rt + 8 e + lane / 8, chunk
   // lane % 8 (K [8 (lane % 8), +8)) of each step.
@@ -121,7 +139,7 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], oob_unless(ok, woff + 16u * e));
+      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], oob_unless(ok, woff + e * w_step8));
 #pragma unroll
     for (int rt = 0; rt < MT; ++rt) {
       const uint32_t xoff = x_row[rt] + (uint32_t)st * 128u;
@@ -158,36 +176,38 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
     for (int d = 0; d < STAGES; ++d) {
       DStage<NPROJ, MT>& S = ring[d];
       if (s0 + d < w_end) {
+        // Stage the step's tiles (slot of chunk c of row or column r: c ^ (r % 8)), then read
+        // row or column j, chunks 4 h + e, back; the waits keep this step's reads after its
+        // writes and ahead of the next step's writes.
+        const int wr = lane >> 3, wc = lane & 7;
+#pragma unroll
+        for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ws[(pr * 32 + 8 * e + wr) * 8 + (wc ^ wr)] = S.w[pr][e];
         if constexpr (XLDS) {
-          // stage the tile (slot of chunk c of row r: c ^ (r % 8)), then read row j, chunks
-          // 4 h + e back; the waits keep this step's reads after its writes and ahead of the
-          // next step's writes
-          const int wr = lane >> 3, wc = lane & 7;
 #pragma unroll
           for (int rt = 0; rt < MT; ++rt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) xs[wave][32 * rt + 8 * e + wr][wc ^ wr] = S.x[rt][e];
-          __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            for (int e = 0; e < 4; ++e) xs[(32 * rt + 8 * e + wr) * 8 + (wc ^ wr)] = S.x[rt][e];
+        }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        u32x4 b[NPROJ][4];
 #pragma unroll
-          for (int rt = 0; rt < MT; ++rt) {
-            u32x4 a[4];
+        for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = xs[wave][32 * rt + j][(4 * h + e) ^ (j & 7)];
+          for (int e = 0; e < 4; ++e) b[pr][e] = ws[(pr * 32 + j) * 8 + ((4 * h + e) ^ (j & 7))];
 #pragma unroll
-            for (int pr = 0; pr < NPROJ; ++pr)
+        for (int rt = 0; rt < MT; ++rt) {
+          u32x4 a[4];
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[pr][rt] = mfma32<DT>(a[e], S.w[pr][e], acc[pr][rt]);
-          }
-          __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        } else {
+          for (int e = 0; e < 4; ++e)
+            a[e] = XLDS ? xs[(32 * rt + j) * 8 + ((4 * h + e) ^ (j & 7))] : S.x[rt][e];
 #pragma unroll
           for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-            for (int rt = 0; rt < MT; ++rt)
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                acc[pr][rt] = mfma32<DT>(S.x[rt][e], S.w[pr][e], acc[pr][rt]);
+            for (int e = 0; e < 4; ++e) acc[pr][rt] = mfma32<DT>(a[e], b[pr][e], acc[pr][rt]);
         }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
       load_stage(S, s0 + d + STAGES);
     }
@@ -195,6 +215,7 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
 
   // ---- per row tile: cross-wave reduction (fixed order), then epilogue or split-K -------
   const size_t plane = (size_t)M * N;
+  __syncthreads();  // the reduction buffer reuses the other waves' staging space
 #pragma unroll
   for (int rt = 0; rt < MT; ++rt) {
     if (rt > 0) __syncthreads();
