@@ -55,7 +55,7 @@ __device__ __forceinline__ uint16_t typed_swiglu(float g, float u) {
 template <int MT>
 constexpr int dense_occupancy() { return MT >= 4 ? 1 : 2; }
 
-// Activation tiles of more than one row tile go through LDS: lane j of an MFMA operand needs row
+// Activation tiles above 8 rows go through LDS (XLDS): lane j of an MFMA operand needs row
 // j, so loading the operand directly touches 32 rows (32 cache lines, 32 bytes of each) per
 // instruction; loaded 8 lanes per row instead, every instruction reads 8 whole 128-byte lines
 // (config 2 at M = 128: gate/up 35.5 -> 29.2 us, down 40.0 -> 30.7 us in a probe with the same
@@ -63,28 +63,25 @@ constexpr int dense_occupancy() { return MT >= 4 ? 1 : 2; }
 // in the MFMA layout; the 16-byte chunk c of staged row r sits at slot c ^ (r % 8), so that the
 // eight lanes of a read phase (rows r..r+7, one chunk) hit distinct banks. The operands, and so
 // every MFMA and sum, are the same as with direct loads.
-template <int MT>
-constexpr bool dense_x_lds() { return MT >= 2; }
 
 // LDS of one workgroup, 16-byte units: during the K loop each wave's staged activation tile
 // (XLDS) and weight tile ([NPROJ][32 columns][8 chunks], the same swizzle); after it the
 // cross-wave reduction buffer [kWaves][NPROJ][32][33] (fp32), in the same space.
-template <int MT, int NPROJ>
+template <int MT, int NPROJ, bool XLDS>
 constexpr int dense_lds_units() {
-  constexpr int per_wave = (dense_x_lds<MT>() ? MT * 32 * 8 : 0) + NPROJ * 32 * 8;
+  constexpr int per_wave = (XLDS ? MT * 32 * 8 : 0) + NPROJ * 32 * 8;
   constexpr int loop = kWaves * per_wave;
   constexpr int red = (kWaves * NPROJ * 32 * 33 + 3) / 4;
   return loop > red ? loop : red;
 }
 
-template <int DT, int MT, int NPROJ, int STAGES>
+template <int DT, int MT, int NPROJ, int STAGES, bool XLDS>
 __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_kernel(
     const DenseParams args) {
   const DenseParams p = preload_args(args);  // all arguments in one batch of scalar loads
-  constexpr bool XLDS = dense_x_lds<MT>();
   constexpr int kXUnits = XLDS ? MT * 32 * 8 : 0;  // per wave
   constexpr int kWUnits = NPROJ * 32 * 8;          // per wave
-  __shared__ __attribute__((aligned(16))) u32x4 smem[dense_lds_units<MT, NPROJ>()];
+  __shared__ __attribute__((aligned(16))) u32x4 smem[dense_lds_units<MT, NPROJ, XLDS>()];
   __shared__ int last_flag;
   auto red = reinterpret_cast<float (*)[NPROJ][32][33]>(smem);  // [kWaves][NPROJ][32][33]
 
@@ -299,12 +296,20 @@ constexpr int dense_stages() {
 template <int DT, int NPROJ>
 hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
   const dim3 grid(p.N / 32, p.ksplit);
-  if (p.M <= 32) {
-    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>()><<<grid, kThreads, 0, stream>>>(p);
+  // Activations staged through LDS above 8 rows (at fewer rows most operand lanes read zero
+  // and the direct loads touch few lines).
+  if (p.M <= 8) {
+    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), false>
+        <<<grid, kThreads, 0, stream>>>(p);
+  } else if (p.M <= 32) {
+    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), true>
+        <<<grid, kThreads, 0, stream>>>(p);
   } else if (p.M <= 64) {
-    dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>()><<<grid, kThreads, 0, stream>>>(p);
+    dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>(), true>
+        <<<grid, kThreads, 0, stream>>>(p);
   } else {
-    dense_qmv_kernel<DT, 4, NPROJ, dense_stages<NPROJ, 4>()><<<grid, kThreads, 0, stream>>>(p);
+    dense_qmv_kernel<DT, 4, NPROJ, dense_stages<NPROJ, 4>(), true>
+        <<<grid, kThreads, 0, stream>>>(p);
   }
   return hipGetLastError();
 }
