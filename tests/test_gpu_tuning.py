@@ -69,6 +69,9 @@ QMV_SHAPES = (
         (3, 4864, 896, 64, 4, 1, True),
         (3, 1024, 1536, 32, 8, 2, False),
         (1, 5120, 2048, 64, 8, 1, False),
+        # Llama-3-8B's MLP at one row: 448 strips of gate/up, 224-step down projection
+        (1, 4096, 14336, 64, 4, 2, False),
+        (1, 14336, 4096, 64, 4, 1, True),
     ]
 )
 
