@@ -214,10 +214,12 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   // then a group's rows in row order: read from other lanes of the wave (kWaveGroups) or
   // through LDS.
   if constexpr (LAYOUT == kWaveGroups) {
-    // Every lane ends with its row's sum; a group's rows (at most 4: a group is at most one
-    // wave) are read from their first lanes and added in row order, giving every lane the
-    // group's totals. Lane (j, m) of each group then stores output (m, column j).
-    const int rows16 = (chunks + 15) >> 4;  // rows of 16 lanes per group
+    // A group fills 1, 2 or 4 rows of 16 lanes (4, 2 or 1 groups per wave; with one group per
+    // wave, rows past its chunks hold +0, which leaves a sum unchanged). Each row's sum is
+    // taken within the row, then row broadcasts add the rows of a group: rows 1 and 3 add
+    // rows 0 and 2, and row 3 adds row 1, so group g's totals land in every lane of row
+    // (g + 1) * slot - 1, slot = 4 / gpw, summed as (S0 + S1) + (S2 + S3). Lane j * ROWS + m
+    // of that row stores output (m, column j).
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
@@ -227,42 +229,53 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
           const float v = group_sum8(acc[pr][j][m]);
           acc[pr][j][m] = v + dpp_read<kDppRowRor8>(v);
         }
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-    for (int gl = 0; gl < gpw; ++gl) {
+    // One wave-uniform branch per group shape; within it the slot is a constant.
+    auto finish = [&](auto slot_c) {
+      constexpr int SLOT = decltype(slot_c)::value;
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+        for (int j = 0; j < COLS; ++j)
+#pragma unroll
+          for (int m = 0; m < ROWS; ++m) {
+            float v = acc[pr][j][m];
+            if constexpr (SLOT >= 2) v += dpp_read_rows<kDppRowBcast15, 0xA>(v);
+            if constexpr (SLOT == 4) v += dpp_read_rows<kDppRowBcast31, 0x8>(v);
+            acc[pr][j][m] = v;
+          }
+      const int r = lane >> 4, i = lane & 15;
+      const int j = i / ROWS, m = i % ROWS;
+      if (((r + 1) & (SLOT - 1)) != 0 || i >= COLS * ROWS || m >= M) return;
+      // Lane i picks output i by a chain of selects over register values (made opaque, so
+      // that the compiler does not turn the chain into an indexed access of a private array,
+      // which it places in LDS).
       float mine[NPROJ];
 #pragma unroll
-      for (int pr = 0; pr < NPROJ; ++pr) mine[pr] = 0.0f;
+      for (int pr = 0; pr < NPROJ; ++pr) mine[pr] = opaque(acc[pr][0][0]);
 #pragma unroll
-      for (int j = 0; j < COLS; ++j)
+      for (int k = 1; k < COLS * ROWS; ++k)
 #pragma unroll
-        for (int m = 0; m < ROWS; ++m) {
-#pragma unroll
-          for (int pr = 0; pr < NPROJ; ++pr) {
-            // Rows past the group add +0.0, which leaves the sum unchanged: no branches.
-            const int a = __builtin_bit_cast(int, acc[pr][j][m]);
-            float t = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float rv = __builtin_bit_cast(
-                  float, __builtin_amdgcn_readlane(a, 16 * ((gl * rows16 + r) & 3)));
-              t += r < rows16 ? rv : 0.0f;
-            }
-            if (lane == j * ROWS + m) mine[pr] = t;
-          }
+        for (int pr = 0; pr < NPROJ; ++pr) {
+          const float v = opaque(acc[pr][k / ROWS][k % ROWS]);
+          mine[pr] = i == k ? v : mine[pr];
         }
-      const int j = lane / ROWS, m = lane % ROWS;
-      if (lane < COLS * ROWS && m < M) {
-        const size_t o = (size_t)m * N + (wg * groups + wave_u * gpw + gl) * COLS + j;
-        float out;
-        if constexpr (NPROJ == 2) {
-          out = silu_mul(mine[0], mine[1]);
-        } else {
-          out = mine[0];
-          if (p.residual) out += act_to_f32<DT>(p.residual[o]);
-        }
-        p.y[o] = f32_to_act<DT>(out);
+      const int g = r / SLOT;
+      const size_t o = (size_t)m * N + (wg * groups + wave * gpw + g) * COLS + j;
+      float out;
+      if constexpr (NPROJ == 2) {
+        out = silu_mul(mine[0], mine[1]);
+      } else {
+        out = mine[0];
+        if (p.residual) out += act_to_f32<DT>(p.residual[o]);
       }
-    }
+      p.y[o] = f32_to_act<DT>(out);
+    };
+    if (gpw >= 4)
+      finish(IntConst<1>{});
+    else if (gpw == 2)
+      finish(IntConst<2>{});
+    else
+      finish(IntConst<4>{});
   } else {
     __shared__ float red[kGemvMaxWaves][kOut][4];  // per wave, output and row of 16 lanes
 #pragma unroll

@@ -273,6 +273,30 @@ __device__ __forceinline__ float dpp_read(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// ---- across rows of 16 lanes: row broadcasts (rows outside ROW_MASK read +0) ----
+// kDppRowBcast15: a row reads lane 15 of the row before it; kDppRowBcast31: rows 2 and 3 read
+// lane 31.
+constexpr int kDppRowBcast15 = 0x142;  // row_bcast:15
+constexpr int kDppRowBcast31 = 0x143;  // row_bcast:31
+
+// The value unchanged, opaque to the optimizer (an empty asm that may rewrite the register).
+__device__ __forceinline__ float opaque(float v) {
+  __asm__ volatile("" : "+v"(v));
+  return v;
+}
+
+// A compile-time int carried as a type (to instantiate a generic lambda per value).
+template <int V>
+struct IntConst {
+  static constexpr int value = V;
+};
+
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_read_rows(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                               CTRL, ROW_MASK, 0xF, false));
+}
+
 // Sum over each aligned group of 4 (or 8) lanes; every lane of the group receives it. The
 // additions pair the same operands as xor exchanges over 1, 2 (and 4) would: lanes of a quad
 // hold the same quad sum, so the half mirror's partner quad is the xor-4 one.
