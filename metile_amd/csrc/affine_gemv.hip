@@ -211,8 +211,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   }
 
   // Rows of 16 lanes by DPP (each lane ends with its row's sum; a row never spans two groups),
-  // then a group's rows in row order: read from other lanes of the wave (kWaveGroups) or
-  // through LDS.
+  // then a group's rows: by row broadcasts within the wave (kWaveGroups; kOneGroup, whose
+  // waves' sums then meet in LDS), or in row order through LDS (kStraddle).
   if constexpr (LAYOUT == kWaveGroups) {
     // A group fills 1, 2 or 4 rows of 16 lanes (4, 2 or 1 groups per wave; with one group per
     // wave, rows past its chunks hold +0, which leaves a sum unchanged). Each row's sum is
@@ -276,7 +276,50 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
       finish(IntConst<2>{});
     else
       finish(IntConst<4>{});
+  } else if constexpr (LAYOUT == kOneGroup) {
+    // One group over all the workgroup's lanes: each wave adds its rows by row broadcasts
+    // ((S0 + S1) + (S2 + S3), rows past K hold +0) and its last lane leaves the wave's sum
+    // in LDS; the waves' sums are then added in wave order.
+    __shared__ float red[kGemvMaxWaves][kOut];
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+      for (int j = 0; j < COLS; ++j)
+#pragma unroll
+        for (int m = 0; m < ROWS; ++m) {
+          float v = group_sum8(acc[pr][j][m]);
+          v += dpp_read<kDppRowRor8>(v);
+          v += dpp_read_rows<kDppRowBcast15, 0xA>(v);
+          v += dpp_read_rows<kDppRowBcast31, 0x8>(v);
+          if (lane == 63) red[wave][(pr * COLS + j) * ROWS + m] = v;
+        }
+    __syncthreads();
+    if (tid < COLS * ROWS) {
+      const int j = tid / ROWS, m = tid % ROWS;
+      float v[NPROJ];
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr) {
+        const int o = (pr * COLS + j) * ROWS + m;
+        float s = red[0][o];
+#pragma unroll
+        for (int w = 1; w < kGemvMaxWaves; ++w)
+          if (w < waves) s += red[w][o];
+        v[pr] = s;
+      }
+      if (m < M) {
+        const size_t o = (size_t)m * N + wg * COLS + j;
+        float out;
+        if constexpr (NPROJ == 2) {
+          out = silu_mul(v[0], v[1]);
+        } else {
+          out = v[0];
+          if (p.residual) out += act_to_f32<DT>(p.residual[o]);
+        }
+        p.y[o] = f32_to_act<DT>(out);
+      }
+    }
   } else {
+    // Groups straddling waves (kStraddle): row sums through LDS, a group's rows in row order.
     __shared__ float red[kGemvMaxWaves][kOut][4];  // per wave, output and row of 16 lanes
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
@@ -291,8 +334,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
     __syncthreads();
     if (tid < groups * COLS * ROWS) {
       const int g = tid / (COLS * ROWS), j = (tid / ROWS) % COLS, m = tid % ROWS;
-      const int r0 = GROUPS ? g * (chunks / 16) : 0;
-      const int r1 = GROUPS ? r0 + chunks / 16 : 4 * waves;
+      const int r0 = g * (chunks / 16);
+      const int r1 = r0 + chunks / 16;
       float v[NPROJ];
 #pragma unroll
       for (int pr = 0; pr < NPROJ; ++pr) {
