@@ -123,7 +123,9 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   // ---- activation chunks: chunk c = row * cpr + cc holds elements [8 cc, 8 cc + 8) --------
   const int cpr = steps_here * 8;
   const int nchunks = M * cpr;
-  const float inv_cpr = 1.0f / (float)cpr;
+  // (c + 1/2) / cpr stays at least 1 / (2 cpr) >= 1/1008 from an integer for c < 32 cpr, far
+  // beyond the hardware reciprocal's error, so the truncated product is the exact row.
+  const float inv_cpr = __builtin_amdgcn_rcpf((float)cpr);
   u32x4 xv[kXIters];
   auto issue_x = [&]() {
 #pragma unroll
