@@ -34,6 +34,9 @@ struct QmvParams {
   uint32_t step_stride;
   int col_align;             // staged kernels: strip boundaries at multiples of this many
                              // columns (1, or a 128-byte line of repacked codes)
+  int strip_cols;            // staged kernels: the width of every strip when all are equal
+                             // (strip s = columns [s strip_cols, (s + 1) strip_cols)), else 0
+  int groups_per_row;        // K / G
   int order;                 // GEMV kernel: 1 = column groups dealt out XCD by XCD
   int gemv_groups;           // GEMV kernel: column groups per workgroup (affine_gemv_groups)
   int gemv_groups_per_wave;  // GEMV kernel, whole groups in every wave: groups per wave

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
   const int nwords = (g_last - g_beg + 1) / 2 + 1;  // 32-bit words per staged row segment
 
   const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
-  const int groups_per_row = K / p.G;
+  const int groups_per_row = p.groups_per_row;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
   __amdgpu_buffer_rsrc_t rw[NPROJ];
 #pragma unroll

@@ -54,10 +54,17 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   const int h = lane >> 5;
   const int M = p.M, K = p.K, N = p.N;
   // Strip boundaries fall on multiples of p.col_align columns (whole cache lines of the
-  // repacked codes, so no line is fetched by two strips).
-  const int units = N / p.col_align;
-  const int col0 = (int)(((int64_t)strip * units) / p.strips) * p.col_align;
-  const int width = (int)(((int64_t)(strip + 1) * units) / p.strips) * p.col_align - col0;
+  // repacked codes, so no line is fetched by two strips). Equal strips (the host's strip_cols)
+  // skip the two divisions.
+  int col0, width;
+  if (p.strip_cols) {
+    col0 = strip * p.strip_cols;
+    width = p.strip_cols;
+  } else {
+    const int units = N / p.col_align;
+    col0 = (int)(((int64_t)strip * units) / p.strips) * p.col_align;
+    width = (int)(((int64_t)(strip + 1) * units) / p.strips) * p.col_align - col0;
+  }
   const int steps_total = K >> 6;
   const int s_beg = split * p.steps_per_split;
   const int s_end = min(steps_total, s_beg + p.steps_per_split);
@@ -78,7 +85,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   float* xsum = reinterpret_cast<float*>(dyn + lay.xsum);  // [steps_per_split * kHalves][MROWS]
 
   const uint32_t row_bytes = (uint32_t)K * BITS / 8u;
-  const int groups_per_row = K / p.G;
+  const int groups_per_row = p.groups_per_row;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
   __amdgpu_buffer_rsrc_t rw[NPROJ];
 #pragma unroll

@@ -540,6 +540,9 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     p.gemv_groups_per_wave = plan.kernel == MT_QMV_GEMV ? p.gemv_groups / plan.tiles : 0;
     p.gemv_dealt = plan.kernel == MT_QMV_GEMV && plan.order ? plan.strips - plan.strips % 8 : 0;
     set_layout(p, layout, bits);
+    const int units = N / p.col_align;
+    p.strip_cols = units % p.strips == 0 ? units / p.strips * p.col_align : 0;
+    p.groups_per_row = K / group_size;
     hipError_t e;
     if (plan.kernel == MT_QMV_GEMV)
       e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles,
