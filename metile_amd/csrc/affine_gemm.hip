@@ -52,7 +52,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const Gemm
   const int s_end = min(steps, s_beg + p.steps_per_split);
 
   const uint32_t row_bytes = (uint32_t)K / 2u;
-  const int groups_per_row = K / p.G;
+  const int gshift = __builtin_ctz((unsigned)p.G);  // groups are powers of two
+  const int groups_per_row = K >> gshift;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, (uint32_t)N * row_bytes);
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s, (uint32_t)N * groups_per_row * 2u);
@@ -86,7 +87,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const Gemm
     for (int i = 0; i < kAChunks; ++i)
       ra[i] = load16(rx, a_off[i] == kOOB ? kOOB : a_off[i] + (uint32_t)st * 128u);
     rc = load16(rw, b_off == kOOB ? kOOB : b_off + (uint32_t)st * 32u);
-    const uint32_t go = g_off == kOOB ? kOOB : g_off + (uint32_t)((st * kBK) / p.G) * 2u;
+    const uint32_t go = g_off == kOOB ? kOOB : g_off + (uint32_t)((st * kBK) >> gshift) * 2u;
     rsv = load2(rs, go);
     rbv = load2(rb, go);
   };
