@@ -558,12 +558,20 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
 }
 
 constexpr int kDenseRowChunk = 128;  // rows per dense dispatch
+// Within a dispatch, more than kDenseSubChunk rows run as grid chunks of kDenseSubChunk rows
+// (two workgroups per CU instead of one with 128-row tiles); each chunk has its own partial
+// sums (kDenseSubChunk rows) and counters.
+constexpr int kDenseSubChunk = 64;
+
+int dense_row_chunk(int rows) { return rows > kDenseSubChunk ? kDenseSubChunk : 0; }
 
 size_t dense_workspace(int M, int K, int N, int nproj) {
   const Plan plan = plan_split(K, N);
   if (plan.ksplit <= 1) return 0;
   const int rows = M < kDenseRowChunk ? M : kDenseRowChunk;
-  return kCounterBytes + (size_t)plan.ksplit * nproj * rows * N * 4;
+  const int sub = dense_row_chunk(rows);
+  const int ws_rows = sub ? (rows + sub - 1) / sub * sub : rows;
+  return kCounterBytes + (size_t)plan.ksplit * nproj * ws_rows * N * 4;
 }
 
 int check_dense(const char* op, int M, int K, int N, int dtype) {
@@ -574,9 +582,11 @@ int check_dense(const char* op, int M, int K, int N, int dtype) {
   if (K % 64 || N % 32)
     return fail(MT_ERR_INVALID_ARGUMENT,
                 std::string(op) + ": K must be a multiple of 64 and N a multiple of 32");
-  if (N / 32 > kMaxStrips)
+  // Counters for two row chunks of up to kDenseSubChunk rows each.
+  if (N / 32 > kMaxStrips / 2)
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": N larger than " +
-                                             std::to_string(kMaxStrips * 32) + " is unsupported");
+                                             std::to_string(kMaxStrips / 2 * 32) +
+                                             " is unsupported");
   if ((size_t)N * K * 2 >= (1ull << 31) || (size_t)kDenseRowChunk * K * 2 >= (1ull << 31))
     return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": tensor larger than 2 GiB");
   return MT_OK;
@@ -611,6 +621,7 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
     p.N = N;
     p.ksplit = plan.ksplit;
     p.steps_per_split = plan.steps_per_split;
+    p.row_chunk = dense_row_chunk(rows);
     const hipError_t e = mt::launch_dense_qmv(p, dtype, nproj, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, op);
   }

@@ -92,7 +92,18 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
   const int h = lane >> 5;
   const int strip = blockIdx.x;
   const int split = blockIdx.y;
-  const int M = p.M, K = p.K, N = p.N;
+  const int K = p.K, N = p.N;
+  // Row chunk z of the launch: its rows, outputs, partial sums and counters.
+  const int rc = p.row_chunk;
+  const int r0 = rc ? (int)blockIdx.z * rc : 0;
+  const int M = rc ? min(rc, p.M - r0) : p.M;
+  const uint16_t* const xg = p.x + (size_t)r0 * K;
+  uint16_t* const yg = p.y + (size_t)r0 * N;
+  const uint16_t* const resg = p.residual ? p.residual + (size_t)r0 * N : nullptr;
+  float* const partg =
+      p.partial ? p.partial + (size_t)blockIdx.z * p.ksplit * NPROJ * (size_t)(rc ? rc : p.M) * N
+                : nullptr;
+  uint32_t* const cntg = p.counters ? p.counters + (size_t)blockIdx.z * (N / 32) : nullptr;
   const int steps_total = K >> 6;
   const int s_beg = split * p.steps_per_split;
   const int s_end = min(steps_total, s_beg + p.steps_per_split);
@@ -101,7 +112,7 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
   const int w_end = min(s_end, w_beg + per_wave);
 
   const uint32_t row_bytes = (uint32_t)K * 2u;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * K * 2u);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xg, (uint32_t)M * K * 2u);
   __amdgpu_buffer_rsrc_t rw[NPROJ];
 #pragma unroll
   for (int pr = 0; pr < NPROJ; ++pr) rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * row_bytes);
@@ -233,17 +244,17 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
           // stash the full sum for the epilogue below
           red[0][pr][i][c] = v;
         } else {
-          __hip_atomic_store(&p.partial[(size_t)(split * NPROJ + pr) * plane + oi], v,
+          __hip_atomic_store(&partg[(size_t)(split * NPROJ + pr) * plane + oi], v,
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       if (p.ksplit == 1) {
         if constexpr (NPROJ == 2) {
-          p.y[oi] = typed_swiglu<DT>(red[0][0][i][c], red[0][1][i][c]);
+          yg[oi] = typed_swiglu<DT>(red[0][0][i][c], red[0][1][i][c]);
         } else {
           float out = round_act<DT>(red[0][0][i][c]);
-          if (p.residual) out = out + act_to_f32<DT>(p.residual[oi]);
-          p.y[oi] = f32_to_act<DT>(out);
+          if (resg) out = out + act_to_f32<DT>(resg[oi]);
+          yg[oi] = f32_to_act<DT>(out);
         }
       }
     }
@@ -255,7 +266,7 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
   __syncthreads();
   if (tid == 0) {
     const unsigned prev =
-        __hip_atomic_fetch_add(&p.counters[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(&cntg[strip], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last_flag = (prev == (unsigned)(p.ksplit - 1));
   }
   __syncthreads();
@@ -266,18 +277,18 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
     float v[NPROJ];
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr) {
-      v[pr] = sum_partials(p.partial + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
+      v[pr] = sum_partials(partg + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
     }
     if constexpr (NPROJ == 2) {
-      p.y[oi] = typed_swiglu<DT>(v[0], v[1]);
+      yg[oi] = typed_swiglu<DT>(v[0], v[1]);
     } else {
       float out = round_act<DT>(v[0]);
-      if (p.residual) out = out + act_to_f32<DT>(p.residual[oi]);
-      p.y[oi] = f32_to_act<DT>(out);
+      if (resg) out = out + act_to_f32<DT>(resg[oi]);
+      yg[oi] = f32_to_act<DT>(out);
     }
   }
   if (tid == 0)
-    __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&cntg[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Register ring depth: the stages that fit beside the accumulators in the registers of one
@@ -295,16 +306,18 @@ constexpr int dense_stages() {
 
 template <int DT, int NPROJ>
 hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
-  const dim3 grid(p.N / 32, p.ksplit);
+  // Rows per chunk (grid z): the instance is chosen by the rows of one chunk.
+  const int rows = p.row_chunk ? p.row_chunk : p.M;
+  const dim3 grid(p.N / 32, p.ksplit, p.row_chunk ? (p.M + p.row_chunk - 1) / p.row_chunk : 1);
   // Activations staged through LDS above 8 rows (at fewer rows most operand lanes read zero
   // and the direct loads touch few lines).
-  if (p.M <= 8) {
+  if (rows <= 8) {
     dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), false>
         <<<grid, kThreads, 0, stream>>>(p);
-  } else if (p.M <= 32) {
+  } else if (rows <= 32) {
     dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), true>
         <<<grid, kThreads, 0, stream>>>(p);
-  } else if (p.M <= 64) {
+  } else if (rows <= 64) {
     dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>(), true>
         <<<grid, kThreads, 0, stream>>>(p);
   } else {
