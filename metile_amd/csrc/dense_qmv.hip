@@ -11,9 +11,9 @@
 // Row invariance: the value of every output depends only on its own activation row and on an
 // accumulation order fixed by (K, N): the K partition among splits and waves comes from
 // (K, N) alone, every wave accumulates its steps in order through one MFMA chain, and the
-// cross-wave and split-K sums run in a fixed order. Running a row alone or inside a batch of
-// up to 128 rows therefore gives the same bits. Batches larger than 128 rows run in 128-row
-// chunks.
+// cross-wave and split-K sums run in a fixed order. Running a row alone or inside a batch
+// therefore gives the same bits. A launch covers up to 64 rows per grid z index (row chunks,
+// each with its own partial sums and counters); the host dispatches up to 128 rows at a time.
 #include "common.h"
 #include "dense_qmv.h"
 
@@ -49,11 +49,10 @@ __device__ __forceinline__ uint16_t typed_swiglu(float g, float u) {
   return f32_to_act<DT>(act * right);
 }
 
-// Workgroups per CU the kernel is built for: two for up to 64 rows; one for 128-row tiles, whose
-// accumulators (4 row tiles x NPROJ) leave room for a deep register ring only with the CU's
-// whole register file.
+// Workgroups per CU the kernel is built for: two (up to 64 rows, MT <= 2; larger batches run
+// as 64-row chunks, which measured faster than 128-row tiles at one workgroup per CU).
 template <int MT>
-constexpr int dense_occupancy() { return MT >= 4 ? 1 : 2; }
+constexpr int dense_occupancy() { return 2; }
 
 // Activation tiles above 8 rows go through LDS (XLDS): lane j of an MFMA operand needs row
 // j, so loading the operand directly touches 32 rows (32 cache lines, 32 bytes of each) per
@@ -292,14 +291,14 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
 }
 
 // Register ring depth: the stages that fit beside the accumulators in the registers of one
-// wave (256 at two workgroups per CU, 512 at one), with at most 60 loads in flight: the
+// wave (256 at two workgroups per CU), with at most 60 loads in flight: the
 // hardware counts at most 63 outstanding loads per wave, and a ring deeper than that count
 // makes the compiler wait for almost every load before each step.
 template <int NPROJ, int MT>
 constexpr int dense_stages() {
   constexpr int per_stage = 16 * NPROJ + 16 * MT;
   constexpr int loads = 4 * NPROJ + 4 * MT;
-  constexpr int budget = dense_occupancy<MT>() == 1 ? 448 - 16 * NPROJ * MT : 112;
+  constexpr int budget = 112;  // ring registers beside the accumulators at two workgroups per CU
   constexpr int s = budget / per_stage < 60 / loads ? budget / per_stage : 60 / loads;
   return s < 1 ? 1 : (s > 4 ? 4 : s);
 }
@@ -321,8 +320,7 @@ hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
     dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>(), true>
         <<<grid, kThreads, 0, stream>>>(p);
   } else {
-    dense_qmv_kernel<DT, 4, NPROJ, dense_stages<NPROJ, 4>(), true>
-        <<<grid, kThreads, 0, stream>>>(p);
+    return hipErrorInvalidValue;  // more than 64 rows run as row chunks (row_chunk)
   }
   return hipGetLastError();
 }
