@@ -89,7 +89,7 @@ def weights():
             "dt": act_to_torch(d, "bf16")}
 
 
-@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 128])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32, 100, 128])
 def test_dense_swiglu_config2(weights, m):
     x = O.make_activations(m, H, 2)
     want = O.dense_swiglu(x, weights["g"], weights["u"])
@@ -122,7 +122,8 @@ def test_dense_projection_without_residual_and_f16():
                 O.dense_residual_exact(x, w, None, dtype="f16"), "f16")
 
 
-@pytest.mark.parametrize("m", [2, 5, 16, 33, 64, 128, 130])
+# 65 and 100 rows: a second 64-row grid chunk of 1 and 36 rows
+@pytest.mark.parametrize("m", [2, 5, 16, 33, 64, 65, 100, 128, 130])
 def test_dense_rows_bit_identical_to_single_row_runs(weights, m):
     x = act_to_torch(O.make_activations(m, H, 3), "bf16")
     r = act_to_torch(O.make_activations(m, H, 3, tensor_id=3), "bf16")
@@ -130,7 +131,8 @@ def test_dense_rows_bit_identical_to_single_row_runs(weights, m):
     u = mt.DenseWeight.from_torch(weights["ut"])
     batch_h = mt.mlx_dense_swiglu(x, g, u)
     batch_y = mt.mlx_dense_residual_qmv(batch_h, weights["dt"], r)
-    rows = range(m) if m <= 16 else sorted({0, 1, m // 2, m - 2, m - 1, 31 % m, 32 % m})
+    rows = range(m) if m <= 16 else sorted({0, 1, m // 2, m - 2, m - 1, 31 % m, 32 % m,
+                                            63 % m, 64 % m, 65 % m})
     for row in rows:
         one_h = mt.mlx_dense_swiglu(x[row:row + 1], g, u)
         one_y = mt.mlx_dense_residual_qmv(one_h, weights["dt"], r[row:row + 1])
