@@ -188,7 +188,7 @@ size_t mt_dense_workspace_bytes(int M, int K, int N, int nproj);
  * operation rounded to that type (metile/compiler/dense.py:193-299 with
  * metile/codegen/msl_emitter.py:1218-1252; entry mlx_dense_swiglu,
  * metile/backends/mlx_dense_swiglu.py:424-491). Each output row is bit-identical whatever
- * M is. K % 64 == 0, N % 32 == 0. */
+ * M is. K % 64 == 0, N % 32 == 0, N <= 262144. */
 int mt_dense_swiglu(const void* x, const void* gate_w, const void* up_w, void* h, int M, int K,
                     int N, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -196,7 +196,7 @@ int mt_dense_swiglu(const void* x, const void* gate_w, const void* up_w, void* h
  * value is rounded to the activation type T before the residual add
  * (metile/compiler/dense.py:302-381, metile/codegen/msl_emitter.py:1098-1120; entry
  * mlx_dense_residual_qmv, metile/backends/mlx_dense_residual.py:276-319). Each output row is
- * bit-identical whatever M is. */
+ * bit-identical whatever M is. K % 64 == 0, N % 32 == 0, N <= 262144. */
 int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, void* y, int M,
                           int K, int N, int dtype, void* workspace, size_t workspace_bytes,
                           void* stream);
