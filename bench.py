@@ -467,7 +467,8 @@ def section_prefill(mt, gen, device, stream, args):
 
 
 def section_ceiling(mt, device, stream, args):
-    """Measured streaming ceilings (``mt_stream_read``: grid-stride 16-byte loads, no tail):
+    """Measured streaming ceilings (``mt_stream_read`` / ``mt_stream_read_blocked``: 16-byte
+    loads in either layout, no tail, the faster kept):
     one launch over distinct buffers of each byte count; the headline step's structure (two
     dependent launches per layer, 15.5 MB then 7.8 MB, 28 distinct layers); and the launch
     floor (one launch reading 16 bytes)."""
@@ -476,30 +477,32 @@ def section_ceiling(mt, device, stream, args):
     lib = _lib.lib()
     sink = torch.empty(65536, dtype=torch.int32, device=device)
 
-    def reads(pairs, blocks):
+    def reads(pairs, blocks, fn=lib.mt_stream_read):
         def run():
             cur = torch.cuda.current_stream(device).cuda_stream
             for buf, nbytes in pairs:
-                _lib.check(lib.mt_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks,
-                                              cur))
+                _lib.check(fn(buf.data_ptr(), nbytes, sink.data_ptr(), blocks, cur))
             return [sink]
         return run
 
     def best(pairs, calls):
         top = None
-        # fixed grids (several batches per thread at large sizes), and grids that cover the
-        # largest buffer in one batch of 1, 2, 4 or 8 loads per thread
+        # both layouts (grid-stride; blocked: each block a contiguous run), fixed grids (several
+        # batches per thread at large sizes) and grids that cover the largest buffer in one
+        # batch of 1, 2, 4 or 8 loads per thread
         big = max(nbytes for _, nbytes in pairs)
         sized = [min(65536, -(-big // (4096 * u))) for u in (1, 2, 4, 8)]
-        for blocks in dict.fromkeys([1024, 2048, 4096, *sized]):
-            with torch.cuda.stream(stream):
-                run = reads(pairs, blocks)
-                run()
-                torch.cuda.synchronize()
-                g = capture(run, stream)
-                us = time_graph(g, stream, max(10, args.steps // 4), args.warmup).mean * 1e3
-            if top is None or us < top[0]:
-                top = (us / calls, blocks)
+        for layout, fn in (("grid-stride", lib.mt_stream_read),
+                           ("blocked", lib.mt_stream_read_blocked)):
+            for blocks in dict.fromkeys([1024, 2048, 4096, *sized]):
+                with torch.cuda.stream(stream):
+                    run = reads(pairs, blocks, fn)
+                    run()
+                    torch.cuda.synchronize()
+                    g = capture(run, stream)
+                    us = time_graph(g, stream, max(10, args.steps // 4), args.warmup).mean * 1e3
+                if top is None or us / calls < top[0]:
+                    top = (us / calls, blocks, layout)
         return top
 
     out = {}
@@ -507,14 +510,16 @@ def section_ceiling(mt, device, stream, args):
                           ("94.7MB", 94_744_576), ("100.7MB", 100_663_296)):
         copies = copies_for(nbytes)
         bufs = [torch.ones(nbytes, dtype=torch.uint8, device=device) for _ in range(copies)]
-        us, blocks = best([(b, nbytes) for b in bufs], copies)
-        out[label] = {"us": round(us, 3), "GBps": rate(nbytes, us), "blocks": blocks}
+        us, blocks, layout = best([(b, nbytes) for b in bufs], copies)
+        out[label] = {"us": round(us, 3), "GBps": rate(nbytes, us), "blocks": blocks,
+                      "layout": layout}
         del bufs
     a, b = 15_503_872, 7_765_504
     layers = [(torch.ones(a, dtype=torch.uint8, device=device),
                torch.ones(b, dtype=torch.uint8, device=device)) for _ in range(LAYERS)]
-    us, blocks = best([p for la, lb in layers for p in ((la, a), (lb, b))], LAYERS)
-    out["two_launch_layer"] = {"us": round(us, 3), "GBps": rate(a + b, us), "blocks": blocks}
+    us, blocks, layout = best([p for la, lb in layers for p in ((la, a), (lb, b))], LAYERS)
+    out["two_launch_layer"] = {"us": round(us, 3), "GBps": rate(a + b, us), "blocks": blocks,
+                               "layout": layout}
     del layers
     tiny = torch.ones(4096, dtype=torch.uint8, device=device)
     with torch.cuda.stream(stream):

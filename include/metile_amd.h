@@ -280,6 +280,12 @@ const char* mt_source_digest(void);
  * is the analogue of its measured streaming-read constant (metile/target/agx.py:38). */
 int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream);
 
+/* The same probe with each block reading its own contiguous run (U x 4 KiB per batch, U as
+ * above), the access pattern of kernels whose workgroups own whole columns of codes. No
+ * counterpart entry point in the reference (metile/target/agx.py:38). */
+int mt_stream_read_blocked(const void* p, size_t bytes, uint32_t* sink, int blocks,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,7 @@ SIGNATURES = {
     "mt_affine_gemm_workspace_bytes": (_Z, [_I, _I, _I, _I, _I]),
     "mt_affine_gemm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_stream_read": (_I, [_P, _Z, _P, _I, _P]),
+    "mt_stream_read_blocked": (_I, [_P, _Z, _P, _I, _P]),
     "mt_dense_workspace_bytes": (_Z, [_I, _I, _I, _I]),
     "mt_dense_swiglu": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "mt_dense_residual_qmv": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),

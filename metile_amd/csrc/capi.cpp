@@ -1182,14 +1182,24 @@ int mt_plans_clear(void) {
   return MT_OK;
 }
 
-int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+static int stream_read(const char* op, const void* p, size_t bytes, uint32_t* sink, int blocks,
+                       bool blocked, void* stream) {
   if (!p || !sink || bytes == 0 || bytes >= (1ull << 31) || blocks < 1 || blocks > 65536)
     return fail(MT_ERR_INVALID_ARGUMENT,
-                "mt_stream_read: need a buffer below 2 GiB, a sink and 1..65536 blocks");
-  const hipError_t e = mt::launch_stream_read(p, (uint32_t)bytes, sink, blocks,
+                std::string(op) + ": need a buffer below 2 GiB, a sink and 1..65536 blocks");
+  const hipError_t e = mt::launch_stream_read(p, (uint32_t)bytes, sink, blocks, blocked,
                                               static_cast<hipStream_t>(stream));
-  if (e != hipSuccess) return hip_fail(e, "mt_stream_read");
+  if (e != hipSuccess) return hip_fail(e, op);
   return MT_OK;
+}
+
+int mt_stream_read(const void* p, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  return stream_read("mt_stream_read", p, bytes, sink, blocks, false, stream);
+}
+
+int mt_stream_read_blocked(const void* p, size_t bytes, uint32_t* sink, int blocks,
+                           void* stream) {
+  return stream_read("mt_stream_read_blocked", p, bytes, sink, blocks, true, stream);
 }
 
 }  // extern "C"

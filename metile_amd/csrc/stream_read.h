@@ -7,6 +7,6 @@
 namespace mt {
 
 hipError_t launch_stream_read(const void* p, uint32_t bytes, uint32_t* sink, int blocks,
-                              hipStream_t stream);
+                              bool blocked, hipStream_t stream);
 
 }  // namespace mt

@@ -88,5 +88,6 @@ def test_stream_read_argument_checks_without_gpu():
     for p, nbytes, sink, blocks in ((None, 4096, buf, 1), (buf, 0, buf, 1), (buf, 1 << 31, buf, 1),
                                     (buf, 4096, None, 1), (buf, 4096, buf, 0),
                                     (buf, 4096, buf, 65537)):
-        assert lib.mt_stream_read(p, nbytes, sink, blocks, None) == _lib.MT_ERR_INVALID_ARGUMENT
-        assert "below 2 GiB" in lib.mt_last_error().decode()
+        for fn in (lib.mt_stream_read, lib.mt_stream_read_blocked):
+            assert fn(p, nbytes, sink, blocks, None) == _lib.MT_ERR_INVALID_ARGUMENT
+            assert "below 2 GiB" in lib.mt_last_error().decode()
