@@ -91,3 +91,18 @@ def test_stream_read_argument_checks_without_gpu():
         for fn in (lib.mt_stream_read, lib.mt_stream_read_blocked):
             assert fn(p, nbytes, sink, blocks, None) == _lib.MT_ERR_INVALID_ARGUMENT
             assert "below 2 GiB" in lib.mt_last_error().decode()
+
+
+def test_dense_workspace_covers_both_row_chunks():
+    """Dense dispatches of more than 64 rows run as two 64-row grid chunks, each with its own
+    split-K partials and counters: the workspace of 65..128 rows holds 128 rows of partials,
+    and a dispatch's workspace never depends on more than 128 rows."""
+    lib = _lib.lib()
+    k, n = 8192, 2048  # the config-2 down projection: split along K
+    ws = {m: lib.mt_dense_workspace_bytes(m, k, n, 1) for m in (1, 64, 65, 100, 128, 129, 1000)}
+    counters = 64 * 1024
+    per_row = (ws[64] - counters) // 64
+    assert ws[1] == counters + per_row
+    assert ws[65] == ws[100] == ws[128] == counters + 128 * per_row
+    assert ws[129] == ws[1000] == ws[128]
+    assert lib.mt_dense_workspace_bytes(4, 2048, 8192, 2) == 0  # gate/up: one K split
