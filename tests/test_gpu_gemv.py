@@ -64,6 +64,8 @@ CASES = [  # (K, N, group, bits, dtype, nproj, residual)
     (1024, 1536, 64, 8, "f16", 2, False),
     (2624, 640, 32, 4, "bf16", 1, False),    # 82 chunks: ragged last pass at every width
     (256, 96, 128, 8, "f16", 1, True),       # 16 chunks, shorter than any pass
+    (1024, 1536, 64, 4, "bf16", 2, False),   # 32 chunks: two column groups per wave
+    (512, 640, 64, 8, "f16", 1, True),       # 32 chunks at 8 bits
 ]
 
 
