@@ -621,16 +621,22 @@ TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "prof
 
 
 def measured_traffic():
-    """HBM bytes per launch of the headline kernel from the committed counter summary (the
-    line ``traffic_bytes_per_launch: N``), or None when that summary is absent."""
+    """``(bytes, kernel)``: HBM bytes per launch of the headline kernel from the committed
+    counter summary (the line ``traffic_bytes_per_launch: N``) and the kernel instance and grid
+    it was measured on (the line ``kernel: ...``), each None when absent. Counter runs need
+    their own processes (rocprofv3 --pmc), so the figure comes from that summary; the JSON line
+    says whether its kernel is the one this run timed."""
+    found = {}
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":", 1)[1].strip())
+                key, _, value = line.partition(":")
+                if key in ("traffic_bytes_per_launch", "kernel") and key not in found:
+                    found[key] = value.strip()
     except OSError:
-        return None
-    return None
+        return None, None
+    nbytes = found.get("traffic_bytes_per_launch")
+    return (int(nbytes) if nbytes else None), found.get("kernel")
 
 
 def cpu_model() -> str:
@@ -783,6 +789,7 @@ def main():
         ceiling = section_ceiling(mt, device, stream, args)
 
     sw, dn = kernel["swiglu"], kernel["down"]
+    traffic_bytes, traffic_kernel = measured_traffic()
     achieved = kernel["swiglu_bytes"] / sw.mean / 1e3
     step_ms = step.mean * LAYERS / 1e3
     value = LAYERS * mlp_bytes(1) / (step_ms * 1e-3) / 1e9
@@ -794,7 +801,9 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": measured_traffic(),
+        "traffic": traffic_bytes,
+        "traffic_kernel": traffic_kernel,
+        "traffic_kernel_is_timed_kernel": traffic_kernel == kernel["swiglu_label"],
         "avg_kernel_us": round(sw.mean, 3),
         "kernel_us_p10_p50_p90": [round(sw.p10, 3), round(sw.p50, 3), round(sw.p90, 3)],
         "bytes_per_launch": kernel["swiglu_bytes"],

@@ -172,6 +172,11 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const Gemm
   }
 
   // ---- epilogue: fp32 tile -> activation type (or split-K fp32 partials) -----------------
+  // Partials go out as device-coherent buffer stores (cache policy sc1), all in flight at once;
+  // one wait below covers them before the arrival counter moves. (As relaxed atomic stores each
+  // had waited for the one before it: 16 to 64 serialized stores per lane.)
+  const __amdgpu_buffer_rsrc_t rp =
+      make_rsrc(p.partial, p.ksplit > 1 ? (uint32_t)p.ksplit * (uint32_t)M * (uint32_t)N * 4u : 0u);
 #pragma unroll
   for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -184,8 +189,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void affine_gemm_kernel(const Gemm
           if (p.ksplit == 1) {
             p.y[(size_t)row * N + col] = f32_to_act<DT>(acc[a][b][r]);
           } else {
-            __hip_atomic_store(&p.partial[((size_t)blockIdx.z * M + row) * N + col],
-                               acc[a][b][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // (__float_as_uint: __builtin_bit_cast of a vector element reads its first word.)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                __float_as_uint(acc[a][b][r]), rp,
+                (((uint32_t)blockIdx.z * M + row) * (uint32_t)N + col) * 4u, 0, kDeviceScope);
           }
         }
       }

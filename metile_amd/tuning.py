@@ -14,7 +14,10 @@ What differs from the reference, by design:
 * The baseline every candidate must beat is the planner's own plan (the reference's is MLX's
   native kernel). A candidate replaces it only when it is faster by ``SWITCH_MARGIN``; within
   ``TIE_TOLERANCE`` of the fastest the plan with the fewest workgroups wins (fewer partial sums),
-  the analogue of the reference's shortest-description tie break.
+  the analogue of the reference's shortest-description tie break, and among those the first in
+  a fixed order of the plans (their text), never the noisier time. The tolerance (1.5%) is wider
+  than the run-to-run spread of one plan's time across boxes, so that near-equal plans resolve
+  the same way from run to run, and profiles taken in another process time the same plan.
 * Candidates are timed as the hot path runs: each plan's dispatches are captured once in a HIP
   graph over enough copies of the weights (``COLD_BYTES``, more than twice the 256 MB Infinity
   Cache) that every dispatch streams its weights from HBM, and the graphs are replayed in a
@@ -51,9 +54,9 @@ import torch
 
 from . import _lib
 
-TUNER_VERSION = 2
+TUNER_VERSION = 3
 SWITCH_MARGIN = 0.02
-TIE_TOLERANCE = 0.0025
+TIE_TOLERANCE = 0.015
 FINALIST_SLACK = 1.10
 TAIL_QUANTILE = 0.75
 SCREEN_ROUNDS = 7
@@ -331,14 +334,15 @@ def head_to_head(candidates, baseline, blocks, measure):
 
 def choose(timings, baseline, cost, *, margin=SWITCH_MARGIN, tie=TIE_TOLERANCE):
     """The key to install: the fastest of the candidates that beat ``baseline`` by ``margin``
-    (within ``tie`` of the fastest, the lowest ``cost(key)``), else ``baseline``."""
+    (within ``tie`` of the fastest, the lowest ``cost(key)``, then the first by ``repr``), else
+    ``baseline``."""
     limit = timings[baseline] * (1.0 - margin)
     eligible = {k: t for k, t in timings.items() if k != baseline and t < limit}
     if not eligible:
         return baseline
     fastest = min(eligible.values())
     tied = [k for k, t in eligible.items() if t <= fastest * (1.0 + tie)]
-    return min(tied, key=lambda k: (cost(k), eligible[k]))
+    return min(tied, key=lambda k: (cost(k), repr(k)))
 
 
 # ---- measuring plans on the GPU -----------------------------------------------------------------
@@ -373,7 +377,7 @@ def _device_identity(device) -> dict:
 def _persistent_key(device, op, shape: dict, candidates) -> str:
     identity = _device_identity(device)
     context = (sorted(identity.items()), [astuple(c) for c in candidates], TUNER_VERSION,
-               SWITCH_MARGIN, TAIL_QUANTILE, COLD_BYTES)
+               SWITCH_MARGIN, TIE_TOLERANCE, TAIL_QUANTILE, COLD_BYTES)
     return decision_key(op, shape, context)
 
 

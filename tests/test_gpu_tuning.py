@@ -121,26 +121,36 @@ def test_every_candidate_plan_matches_the_oracle(shape):
     print(f"[{shape}] {len(cands)} plans, worst tolerance_error {worst:.2e}", flush=True)
 
 
-GEMM_SHAPES = [(200, 1024, 1536), (130, 1536, 896)]
+# The prefill GEMM's plans are held to the contract where the tuner installs them: config 4's
+# two projections at M = 512 (every plan the library lists, the planner's included), and two
+# ragged shapes. Each must be within tolerance_error 2e-3 of the fp32-accumulated oracle over
+# the exact dequantized weights and equal its correctly rounded value in >= 98% of outputs.
+GEMM_SHAPES = [(512, 1536, 8960), (512, 8960, 1536), (200, 1024, 1536), (130, 1536, 896)]
 
 
-@pytest.mark.parametrize("m,k,n", GEMM_SHAPES)
-def test_every_gemm_plan_matches_the_native_composition(m, k, n):
-    w = affine_to_torch(O.make_affine_weight(n, k, 4, 64, 8, 10), "bf16")
-    aw = mt.AffineWeight.from_torch(*w)
-    x = act_to_torch(O.make_activations(m, k, 8), "bf16")
-    want = mt.native_affine_matmul(x, aw)
-    planner = mt.affine_matmul(x, *w)
+@functools.lru_cache(maxsize=1)
+def _gemm_case(m, k, n):
+    w = O.make_affine_weight(n, k, 4, 64, 8, 10)
+    x = O.make_activations(m, k, 8)
+    ref = (O.to_f32(x, "bf16") @ O.dequantize(*w, 64, 4, "bf16").T).astype(np.float64)
+    return w, x, ref
+
+
+@pytest.mark.parametrize("m,k,n", GEMM_SHAPES, ids=lambda v: str(v))
+def test_every_gemm_plan_meets_the_contract(m, k, n):
+    w, x, ref = _gemm_case(m, k, n)
+    wt = affine_to_torch(w, "bf16")
+    xt = act_to_torch(x, "bf16")
     cands = tuning.gemm_plan_candidates(m, k, n, 64)
-    assert len(cands) >= 4
+    assert tuning.gemm_plan(m, k, n, 64, torch.bfloat16) in cands
+    worst = 0.0
     for plan in cands:
+        print(f"[gemm {m}x{k}x{n}] plan {plan}", flush=True)
         tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, plan)
-        y = mt.affine_matmul(x, *w)
+        y = mt.affine_matmul(xt, *wt)
         torch.cuda.synchronize()
-        assert mt.accuracy_compatible(y, want), plan
-        # the same dequantized tiles in another split: a few fp32 roundings apart at most
-        diff = (y.float() - planner.float()).abs().max().item()
-        assert diff <= 2e-2 * planner.float().abs().max().item(), (plan, diff)
+        worst = max(worst, _check(str(plan), torch_to_act(y, "bf16"), ref))
+    print(f"[gemm {m}x{k}x{n}] {len(cands)} plans, worst tolerance_error {worst:.2e}", flush=True)
 
 
 def test_tuner_decides_persists_and_reloads(monkeypatch, tmp_path):

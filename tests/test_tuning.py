@@ -159,9 +159,13 @@ def test_choose_needs_the_margin_and_breaks_ties_by_cost():
     cost = {"base": 0, "a": 10, "b": 5, "c": 1}.__getitem__
     assert tuning.choose({"base": 100.0, "a": 99.0}, "base", cost) == "base"  # 1% < margin
     assert tuning.choose({"base": 100.0, "a": 95.0}, "base", cost) == "a"
-    # a and b within the tie tolerance: fewer workgroups wins; c is not tied
-    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 90.1, "c": 93.0}, "base", cost) == "b"
-    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 91.0}, "base", cost) == "a"
+    # a and b within the tie tolerance (1.5%): fewer workgroups wins; c is not tied
+    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 91.2, "c": 93.0}, "base", cost) == "b"
+    assert tuning.choose({"base": 100.0, "a": 90.0, "b": 92.0}, "base", cost) == "a"
+    # equal cost within the tolerance: the first by text, whichever measured faster
+    same = {"base": 0, "p2": 3, "p1": 3}.__getitem__
+    assert tuning.choose({"base": 100.0, "p1": 90.5, "p2": 90.0}, "base", same) == "p1"
+    assert tuning.choose({"base": 100.0, "p1": 90.0, "p2": 90.5}, "base", same) == "p1"
 
 
 # ---- the plan table of the C ABI (host-only) -----------------------------------------------------
