@@ -410,28 +410,53 @@ def section_qmv(mt, gen, device, stream, args, k, n, bits, rows):
     return {"K": k, "N": n, "bits": bits, "copies": copies, "rows": out}
 
 
+DENSE_ROWS = (1, 2, 4, 8, 16, 32, 64, 128)
+
+
 def section_dense(mt, gen, device, stream, args):
-    """Dense BF16 SwiGLU MLP at Llama-3.2-1B shape (config 2)."""
+    """Dense BF16 SwiGLU MLP at Llama-3.2-1B shape (config 2) at every BASELINE row count (and
+    64), each beside the same MLP in torch's bf16 matmuls over the same weights (the vendor
+    library at the same weight format: the comparator the reference times its dense kernels
+    against). The dense plans are resolved first (``tuning.ensure_dense_plan``: one plan per
+    (K, N), timed over several row counts, which keeps every row bit-identical to that row run
+    alone)."""
     h, i = 2048, 8192
     wbytes = 3 * 2 * h * i
     copies = copies_for(wbytes)
     ws = [tuple((torch.randn(n, k, generator=gen, device=device) * 0.02).to(torch.bfloat16)
                 for n, k in ((i, h), (i, h), (h, i))) for _ in range(copies)]
+    plans = {}
+    if not args.no_tune:
+        from metile_amd import tuning
+
+        g0, u0, d0 = ws[0]
+        tuning.ensure_dense_plan([g0, u0], torch.bfloat16)
+        tuning.ensure_dense_plan([d0], torch.bfloat16)
+        plans = {"gate_up_ksplit": tuning.dense_plan(h, i, 2, torch.bfloat16).ksplit,
+                 "down_ksplit": tuning.dense_plan(i, h, 1, torch.bfloat16).ksplit}
     out = {}
-    for m in (1, 2, 8, 16, 32, 128):
+    for m in DENSE_ROWS:
         x = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
         res = torch.randn(m, h, generator=gen, device=device).to(torch.bfloat16)
 
         def stack():
             return [mt.dense_qmv(mt.dense_swiglu(x, g, u), d, res) for (g, u, d) in ws]
 
-        t = timed(stack, stream, max(10, args.steps // 4), args.warmup, copies)
+        def vendor():
+            f = torch.nn.functional.silu
+            return [(f(x @ g.t()) * (x @ u.t())) @ d.t() + res for (g, u, d) in ws]
+
+        steps = max(10, args.steps // 4)
+        t = timed(stack, stream, steps, args.warmup, copies)
+        tv = timed(vendor, stream, steps, args.warmup, copies)
         total = wbytes + 2 * m * h * 3 + 4 * m * i
         mean, p10, p50, p90 = t.scaled(1.0)
         out[str(m)] = {"us": mean, "p10": p10, "p90": p90, "GBps": rate(total, t.mean),
-                       "frac": round(total / t.mean / 1e3 / HBM_PEAK_GBS, 4)}
+                       "frac": round(total / t.mean / 1e3 / HBM_PEAK_GBS, 4),
+                       "torch_bf16_us": round(tv.mean, 3),
+                       "vs_torch_bf16": round(tv.mean / t.mean, 3)}
     del ws
-    return {"hidden": h, "intermediate": i, "copies": copies, "rows": out}
+    return {"hidden": h, "intermediate": i, "copies": copies, "plans": plans, "rows": out}
 
 
 def section_prefill(mt, gen, device, stream, args):
@@ -725,11 +750,12 @@ def tuning_report(args):
     for e in tuning.cached_decisions():
         decisions.append({
             "op": e.get("op"), "rows": e.get("rows"), "K": e.get("input_features"),
-            "N": e.get("output_features"), "bits": e.get("bits"), "nproj": e.get("nproj", 1),
+            "N": e.get("output_features"), "bits": e.get("bits"),
+            "nproj": e.get("nproj", e.get("projections", 1)),
             "planner": short(e.get("planner")), "chosen": short(e.get("plan")),
             "planner_us": e.get("planner_us"), "chosen_us": e.get("chosen_us"),
             **({"layout": e["layout"]} if "layout" in e else {})})
-    decisions.sort(key=lambda d: (d["op"], d["nproj"], d["K"], d["N"], d["rows"]))
+    decisions.sort(key=lambda d: (d["op"], d["nproj"], d["K"], d["N"], d["rows"] or 0))
     return decisions
 
 

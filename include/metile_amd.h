@@ -263,6 +263,20 @@ int mt_affine_gemm_plan_candidates(int M, int K, int N, int group_size, mt_gemm_
                                    int capacity);
 int mt_affine_gemm_plan_set(int M, int K, int N, int group_size, int dtype,
                             const mt_gemm_plan* plan);
+/* How a dense projection runs: its K splits. Keyed by (K, N, nproj, dtype) only, so that one
+ * plan serves every row count and each output row stays bit-identical to that row run alone;
+ * the analogue of the reference's tuned dense schedules under its per-row exactness gate
+ * (metile/backends/mlx_dense_swiglu.py:343-421, metile/backends/mlx_dense_residual.py:202-273).
+ * Splits are equal-length runs of at least 4 64-wide K steps, at most 32 of them. */
+typedef struct mt_dense_plan {
+  int ksplit;
+} mt_dense_plan;
+int mt_dense_qmv_plan(int K, int N, int nproj, int dtype, mt_dense_plan* out);
+int mt_dense_qmv_plan_candidates(int K, int N, int nproj, mt_dense_plan* out, int capacity);
+/* Install `plan` for the shape (rejects a plan the kernel cannot run); NULL removes it. The
+ * workspace query (mt_dense_workspace_bytes) covers every installed plan. */
+int mt_dense_qmv_plan_set(int K, int N, int nproj, int dtype, const mt_dense_plan* plan);
+
 /* Remove every installed plan. */
 int mt_plans_clear(void);
 /* SHA-256 of the kernel and boundary sources this library was built from (hex): the part of a

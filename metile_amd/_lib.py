@@ -40,11 +40,18 @@ class GemmPlan(ctypes.Structure):
     _fields_ = [("tile", ctypes.c_int), ("ksplit", ctypes.c_int)]
 
 
+class DensePlan(ctypes.Structure):
+    """``mt_dense_plan``."""
+
+    _fields_ = [("ksplit", ctypes.c_int)]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _Z = ctypes.c_size_t
 _QP = ctypes.POINTER(QmvPlan)
 _GP = ctypes.POINTER(GemmPlan)
+_DP = ctypes.POINTER(DensePlan)
 
 # name -> (restype, argtypes); mirrors include/metile_amd.h exactly.
 SIGNATURES = {
@@ -82,6 +89,9 @@ SIGNATURES = {
     "mt_affine_gemm_plan": (_I, [_I, _I, _I, _I, _I, _GP]),
     "mt_affine_gemm_plan_candidates": (_I, [_I, _I, _I, _I, _GP, _I]),
     "mt_affine_gemm_plan_set": (_I, [_I, _I, _I, _I, _I, _GP]),
+    "mt_dense_qmv_plan": (_I, [_I, _I, _I, _I, _DP]),
+    "mt_dense_qmv_plan_candidates": (_I, [_I, _I, _I, _DP, _I]),
+    "mt_dense_qmv_plan_set": (_I, [_I, _I, _I, _I, _DP]),
     "mt_plans_clear": (_I, []),
     "mt_source_digest": (ctypes.c_char_p, []),
 }

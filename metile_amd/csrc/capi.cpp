@@ -257,11 +257,16 @@ struct PlanKeyHash {
   }
 };
 
-enum PlanOp : int { kOpQmv = 0, kOpGemm = 1 };
+enum PlanOp : int { kOpQmv = 0, kOpGemm = 1, kOpDense = 2 };
 
 std::shared_mutex g_plans_mu;
 std::unordered_map<PlanKey, mt_qmv_plan, PlanKeyHash> g_qmv_plans;
 std::unordered_map<PlanKey, mt_gemm_plan, PlanKeyHash> g_gemm_plans;
+std::unordered_map<PlanKey, mt_dense_plan, PlanKeyHash> g_dense_plans;
+
+int installed_plans() {
+  return (int)(g_qmv_plans.size() + g_gemm_plans.size() + g_dense_plans.size());
+}
 std::atomic<int> g_plans_installed{0};
 
 PlanKey qmv_key(int rows, int K, int N, int nproj, int group_size, int bits, int dtype) {
@@ -565,13 +570,60 @@ constexpr int kDenseSubChunk = 64;
 
 int dense_row_chunk(int rows) { return rows > kDenseSubChunk ? kDenseSubChunk : 0; }
 
+// Dense plans: the K split of every dispatch of a (K, N) shape. Keyed without the rows, so that
+// one plan serves every row count and each row keeps its summation order whatever M is (the
+// per-row bit identity). The planner's is plan_split's; a tuner may install another.
+PlanKey dense_key(int K, int N, int nproj, int dtype) {
+  return PlanKey{kOpDense, 0, K, N, nproj, 0, 16, dtype};
+}
+
+Plan plan_dense(int K, int N, int nproj, int dtype) {
+  if (g_plans_installed.load(std::memory_order_acquire) != 0) {
+    std::shared_lock<std::shared_mutex> lock(g_plans_mu);
+    const auto it = g_dense_plans.find(dense_key(K, N, nproj, dtype));
+    if (it != g_dense_plans.end()) return split_plan(K / 64, it->second.ksplit);
+  }
+  return plan_split(K, N);
+}
+
+// Why `q` cannot run a dense dispatch of this shape ("" when it can): K split into equal-length
+// splits of at least 4 steps (the four waves of a strip each take a contiguous quarter), at most
+// kMaxCandidateSplits.
+std::string dense_plan_problem(int K, const mt_dense_plan& q) {
+  const int steps = K / 64;
+  if (q.ksplit < 1 || q.ksplit > steps || q.ksplit > kMaxCandidateSplits)
+    return "ksplit must be in 1..min(K/64, 32)";
+  const Plan p = split_plan(steps, q.ksplit);
+  if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
+  if (p.steps_per_split < 4) return "each split needs at least 4 K steps (one per wave)";
+  return "";
+}
+
+std::vector<mt_dense_plan> dense_candidates(int K) {
+  std::vector<mt_dense_plan> out;
+  int last = 0;
+  for (int ks = 1; ks <= kMaxCandidateSplits / 2; ++ks) {
+    const Plan p = split_plan(K / 64, ks);
+    if (p.ksplit == last) continue;
+    last = p.ksplit;
+    const mt_dense_plan q{p.ksplit};
+    if (dense_plan_problem(K, q).empty()) out.push_back(q);
+  }
+  return out;
+}
+
 size_t dense_workspace(int M, int K, int N, int nproj) {
-  const Plan plan = plan_split(K, N);
-  if (plan.ksplit <= 1) return 0;
+  // The largest need of the planner's plan and of either dtype's installed plan.
+  int ksplit = plan_split(K, N).ksplit;
+  for (int dtype : {MT_BF16, MT_F16}) {
+    const int ks = plan_dense(K, N, nproj, dtype).ksplit;
+    if (ks > ksplit) ksplit = ks;
+  }
+  if (ksplit <= 1) return 0;
   const int rows = M < kDenseRowChunk ? M : kDenseRowChunk;
   const int sub = dense_row_chunk(rows);
   const int ws_rows = sub ? (rows + sub - 1) / sub * sub : rows;
-  return kCounterBytes + (size_t)plan.ksplit * nproj * ws_rows * N * 4;
+  return kCounterBytes + (size_t)ksplit * nproj * ws_rows * N * 4;
 }
 
 int check_dense(const char* op, int M, int K, int N, int dtype) {
@@ -604,7 +656,7 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
   if (need && (!workspace || workspace_bytes < need))
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
-  const Plan plan = plan_split(K, N);
+  const Plan plan = plan_dense(K, N, nproj, dtype);
   for (int r0 = 0; r0 < M; r0 += kDenseRowChunk) {
     const int rows = (M - r0) < kDenseRowChunk ? (M - r0) : kDenseRowChunk;
     mt::DenseParams p{};
@@ -1121,8 +1173,7 @@ int mt_affine_qmv_plan_set(int M, int K, int N, int group_size, int bits, int np
   std::unique_lock<std::shared_mutex> lock(g_plans_mu);
   if (plan) g_qmv_plans[key] = *plan;
   else g_qmv_plans.erase(key);
-  g_plans_installed.store((int)(g_qmv_plans.size() + g_gemm_plans.size()),
-                          std::memory_order_release);
+  g_plans_installed.store(installed_plans(), std::memory_order_release);
   return MT_OK;
 }
 
@@ -1169,8 +1220,7 @@ int mt_affine_gemm_plan_set(int M, int K, int N, int group_size, int dtype,
   std::unique_lock<std::shared_mutex> lock(g_plans_mu);
   if (plan) g_gemm_plans[key] = *plan;
   else g_gemm_plans.erase(key);
-  g_plans_installed.store((int)(g_qmv_plans.size() + g_gemm_plans.size()),
-                          std::memory_order_release);
+  g_plans_installed.store(installed_plans(), std::memory_order_release);
   return MT_OK;
 }
 
@@ -1178,7 +1228,46 @@ int mt_plans_clear(void) {
   std::unique_lock<std::shared_mutex> lock(g_plans_mu);
   g_qmv_plans.clear();
   g_gemm_plans.clear();
+  g_dense_plans.clear();
   g_plans_installed.store(0, std::memory_order_release);
+  return MT_OK;
+}
+
+static int check_dense_plan_shape(const char* op, int K, int N, int nproj, int dtype) {
+  if (nproj != 1 && nproj != 2)
+    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": nproj must be 1 or 2");
+  return check_dense(op, 1, K, N, dtype);
+}
+
+int mt_dense_qmv_plan(int K, int N, int nproj, int dtype, mt_dense_plan* out) {
+  const int st = check_dense_plan_shape("mt_dense_qmv_plan", K, N, nproj, dtype);
+  if (st) return st;
+  if (!out) return fail(MT_ERR_INVALID_ARGUMENT, "mt_dense_qmv_plan: null output");
+  *out = mt_dense_plan{plan_dense(K, N, nproj, dtype).ksplit};
+  return MT_OK;
+}
+
+int mt_dense_qmv_plan_candidates(int K, int N, int nproj, mt_dense_plan* out, int capacity) {
+  const int st = check_dense_plan_shape("mt_dense_qmv_plan_candidates", K, N, nproj, MT_BF16);
+  if (st) return st;
+  if (capacity < 0 || (capacity > 0 && !out))
+    return fail(MT_ERR_INVALID_ARGUMENT, "mt_dense_qmv_plan_candidates: bad output buffer");
+  const std::vector<mt_dense_plan> c = dense_candidates(K);
+  for (int i = 0; i < (int)c.size() && i < capacity; ++i) out[i] = c[i];
+  return (int)c.size();
+}
+
+int mt_dense_qmv_plan_set(int K, int N, int nproj, int dtype, const mt_dense_plan* plan) {
+  const int st = check_dense_plan_shape("mt_dense_qmv_plan_set", K, N, nproj, dtype);
+  if (st) return st;
+  if (plan) {
+    const std::string why = dense_plan_problem(K, *plan);
+    if (!why.empty()) return fail(MT_ERR_INVALID_ARGUMENT, "mt_dense_qmv_plan_set: " + why);
+  }
+  std::unique_lock<std::shared_mutex> lock(g_plans_mu);
+  if (plan) g_dense_plans[dense_key(K, N, nproj, dtype)] = *plan;
+  else g_dense_plans.erase(dense_key(K, N, nproj, dtype));
+  g_plans_installed.store(installed_plans(), std::memory_order_release);
   return MT_OK;
 }
 

@@ -4,7 +4,10 @@ Mirrors meTile's dense MLX backends (``metile/backends/mlx_dense.py``,
 ``mlx_dense_swiglu.py``, ``mlx_dense_residual.py``): ``DenseWeight`` stands in for
 ``MLXDenseWeight`` and ``mlx_dense_swiglu`` / ``mlx_dense_residual_qmv`` keep the reference
 names, arguments and ``ValueError``/``TypeError`` guards. Every output row is bit-identical to
-running that row alone (the reduction order of each output depends only on K and N).
+running that row alone (the reduction order of each output depends only on the plan of its
+(K, N), which serves every row count). With ``autotune`` the entries first resolve that plan
+(``metile_amd.tuning.ensure_dense_plan``: measured once per shape over several row counts,
+persisted), as the reference's tuned dense entries do.
 """
 
 from __future__ import annotations
@@ -118,6 +121,11 @@ def mlx_dense_swiglu(values, gate_weight, up_weight, *, paired_weight=None, auto
             tuple(paired_weight.shape) != (gate_weight.shape[1], gate_weight.shape[0], 2)
             or paired_weight.dtype != values.dtype):
         raise ValueError("paired dense SwiGLU weight must have shape [N, K, 2] and matching dtype")
+    if autotune:
+        from . import tuning
+
+        tuning.ensure_dense_plan([gate_weight.native_weight, up_weight.native_weight],
+                                 values.dtype)
     return dense_swiglu(values, gate_weight.native_weight, up_weight.native_weight)
 
 
@@ -134,4 +142,8 @@ def mlx_dense_residual_qmv(values, weight, residual, *, autotune=True):
         raise TypeError("dense residual QMV requires matching input dtypes")
     if values.dtype not in _DTYPES:
         raise TypeError("dense residual QMV requires bfloat16 or float16")
+    if autotune:
+        from . import tuning
+
+        tuning.ensure_dense_plan([weight], values.dtype)
     return dense_qmv(values, weight, residual)

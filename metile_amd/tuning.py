@@ -207,6 +207,23 @@ class GemmPlan:
         return -(-rows // self.tile) * -(-n // self.tile) * self.ksplit
 
 
+@dataclass(frozen=True)
+class DensePlan:
+    """One dense projection plan (``mt_dense_plan``): the K splits of every row count."""
+
+    ksplit: int
+
+    def to_c(self) -> _lib.DensePlan:
+        return _lib.DensePlan(self.ksplit)
+
+    @classmethod
+    def from_c(cls, p) -> "DensePlan":
+        return cls(p.ksplit)
+
+    def workgroups(self, n: int) -> int:
+        return n // 32 * self.ksplit
+
+
 def _dtype_code(dtype) -> int:
     return {torch.bfloat16: _lib.MT_BF16, torch.float16: _lib.MT_F16}[dtype]
 
@@ -256,6 +273,28 @@ def gemm_plan_candidates(rows, k, n, group_size) -> list[GemmPlan]:
 def install_gemm_plan(rows, k, n, group_size, dtype, plan) -> None:
     c = None if plan is None else ctypes.byref(plan.to_c())
     _lib.check(_lib.lib().mt_affine_gemm_plan_set(rows, k, n, group_size, _dtype_code(dtype), c))
+
+
+def dense_plan(k, n, nproj, dtype) -> DensePlan:
+    """The plan every dense dispatch of this shape takes now (installed, else the planner's)."""
+    out = _lib.DensePlan()
+    _lib.check(_lib.lib().mt_dense_qmv_plan(k, n, nproj, _dtype_code(dtype), ctypes.byref(out)))
+    return DensePlan.from_c(out)
+
+
+def dense_plan_candidates(k, n, nproj) -> list[DensePlan]:
+    L = _lib.lib()
+    count = L.mt_dense_qmv_plan_candidates(k, n, nproj, None, 0)
+    if count < 0:
+        _lib.check(count)
+    buf = (_lib.DensePlan * max(count, 1))()
+    count = L.mt_dense_qmv_plan_candidates(k, n, nproj, buf, count)
+    return [DensePlan.from_c(buf[i]) for i in range(count)]
+
+
+def install_dense_plan(k, n, nproj, dtype, plan) -> None:
+    c = None if plan is None else ctypes.byref(plan.to_c())
+    _lib.check(_lib.lib().mt_dense_qmv_plan_set(k, n, nproj, _dtype_code(dtype), c))
 
 
 def clear_plans() -> None:
@@ -774,6 +813,98 @@ def ensure_gemm_plan(values, weight, scales, biases, *, group_size, autotune=Tru
             plan, record = _tune_gemm(x, weight, scales, biases, group_size)
             _write_decision(key, plan, {"op": "affine_matmul", **shape, **record})
         install_gemm_plan(rows, k, n, group_size, values.dtype, plan)
+        _decided[mem] = plan
+        _resolved[mem] = "cached" if found else "measured"
+        return plan
+
+
+# Row counts a dense plan is timed at: one plan serves every row count (the per-row bit
+# identity), so each candidate's graph holds one dispatch at each of them and is scored on the sum.
+DENSE_TUNING_ROWS = (1, 16, 128)
+
+
+def _tune_dense(weights, dtype):
+    L = _lib.lib()
+    nproj = len(weights)
+    n, k = weights[0].shape
+    device = weights[0].device
+    candidates = dense_plan_candidates(k, n, nproj)
+    copies = _copies(_tensor_bytes(*weights))
+    rotation = [tuple(weights)] + [tuple(w.clone() for w in weights) for _ in range(copies - 1)]
+    need = 0
+    for plan in [None, *candidates]:
+        install_dense_plan(k, n, nproj, dtype, plan)
+        need = max(need, L.mt_dense_workspace_bytes(max(DENSE_TUNING_ROWS), k, n, nproj))
+    install_dense_plan(k, n, nproj, dtype, None)
+    bench = _Bench(device, need)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(0)
+    xs = [torch.randn(m, k, generator=gen, device=device).to(dtype) for m in DENSE_TUNING_ROWS]
+    res = [torch.randn(m, n, generator=gen, device=device).to(dtype) for m in DENSE_TUNING_ROWS]
+    outs = [torch.empty(m, n, dtype=dtype, device=device) for m in DENSE_TUNING_ROWS]
+    code = _dtype_code(dtype)
+
+    def body():
+        stream = torch.cuda.current_stream(device).cuda_stream
+        for x, r, out in zip(xs, res, outs):
+            for ws in rotation:
+                if nproj == 2:
+                    _lib.check(L.mt_dense_swiglu(x.data_ptr(), ws[0].data_ptr(), ws[1].data_ptr(),
+                                                 out.data_ptr(), x.shape[0], k, n, code,
+                                                 bench.ws.data_ptr(), bench.ws.numel(), stream))
+                else:
+                    _lib.check(L.mt_dense_residual_qmv(
+                        x.data_ptr(), ws[0].data_ptr(), r.data_ptr(), out.data_ptr(), x.shape[0],
+                        k, n, code, bench.ws.data_ptr(), bench.ws.numel(), stream))
+
+    graphs, reference = {}, None
+    try:
+        for key, plan in [(_BASELINE, None), *[(c, c) for c in candidates]]:
+            install_dense_plan(k, n, nproj, dtype, plan)
+            graphs[key] = bench.capture(body)
+            bench.stream.synchronize()
+            if reference is None:
+                reference = outs[-1].clone()
+            else:
+                _gate(outs[-1], reference, "dense plan tuning")
+        install_dense_plan(k, n, nproj, dtype, None)
+        timings, chosen = _tournament(bench, graphs, copies,
+                                      lambda key: -1 if key == _BASELINE else key.workgroups(n))
+    finally:
+        install_dense_plan(k, n, nproj, dtype, None)
+        bench.close()
+    planner = dense_plan(k, n, nproj, dtype)
+    plan = None if chosen == _BASELINE else chosen
+    return plan, {"planner": asdict(planner), "planner_us": round(timings[_BASELINE] * 1e6, 3),
+                  "chosen_us": round(timings[chosen] * 1e6, 3), "copies": copies,
+                  "rows_timed": list(DENSE_TUNING_ROWS)}
+
+
+def ensure_dense_plan(weights, dtype, *, autotune=True, retune=False):
+    """The dense plan of a shape (``weights``: the ``[N, K]`` gate and up matrices, or one
+    projection's), measured once per process and persisted like the affine decisions. The
+    decision is keyed by (K, N, projections, dtype) only and installed for every row count, so
+    that each output row stays bit-identical to that row run alone. Returns the plan (None:
+    the planner's)."""
+    nproj = len(weights)
+    n, k = weights[0].shape
+    device = weights[0].device
+    with _lock:
+        mem = ("dense", device.index, k, n, nproj, dtype)
+        if mem in _decided and not retune:
+            return _decided[mem]
+        candidates = dense_plan_candidates(k, n, nproj)
+        shape = {"input_features": k, "output_features": n, "projections": nproj,
+                 "dtype": str(dtype), "rows_timed": list(DENSE_TUNING_ROWS)}
+        key = _persistent_key(device, "dense", shape, candidates)
+        found, plan = (False, None) if retune else _read_decision(key, DensePlan)
+        if not found:
+            if not autotune or not tuning_enabled() or torch.cuda.is_current_stream_capturing():
+                _resolved.setdefault(mem, "planner")
+                return None
+            plan, record = _tune_dense([w.contiguous() for w in weights], dtype)
+            _write_decision(key, plan, {"op": "dense", **shape, **record})
+        install_dense_plan(k, n, nproj, dtype, plan)
         _decided[mem] = plan
         _resolved[mem] = "cached" if found else "measured"
         return plan

@@ -19,7 +19,7 @@ import torch
 
 import metile_amd._lib as L
 from metile_amd import build, tuning
-from metile_amd.tuning import GemmPlan, QmvPlan
+from metile_amd.tuning import DensePlan, GemmPlan, QmvPlan
 
 
 # ---- decision log --------------------------------------------------------------------------------
@@ -432,3 +432,44 @@ def test_layout_choice_argument_checks():
         tuning.ensure_qmv_layout(x, {"packed": packed, "mlx": mlx}, group_size=64, bits=4)
     with pytest.raises(ValueError, match="not in that layout"):
         tuning.ensure_qmv_layout(x, {"repacked": mlx, "mlx": packed}, group_size=64, bits=4)
+
+
+# ---- dense plans (host-only) ---------------------------------------------------------------------
+
+
+def test_dense_plans_are_keyed_by_shape_only_and_size_the_workspace(clean_plans):
+    import torch
+
+    lib = L.lib()
+    k, n = 8192, 2048
+    planner = tuning.dense_plan(k, n, 1, torch.bfloat16)
+    cands = tuning.dense_plan_candidates(k, n, 1)
+    # every split of 128 steps into equal runs of at least 4 steps, at most 16 candidates
+    splits = sorted({-(-128 // -(-128 // ks)) for ks in range(1, 17)})
+    assert [c.ksplit for c in cands] == splits
+    assert planner in cands
+    other = max(cands, key=lambda c: c.ksplit)
+    before = lib.mt_dense_workspace_bytes(128, k, n, 1)
+    tuning.install_dense_plan(k, n, 1, torch.bfloat16, other)
+    assert tuning.dense_plan(k, n, 1, torch.bfloat16) == other
+    assert tuning.dense_plan(k, n, 1, torch.float16) == planner     # per dtype
+    assert tuning.dense_plan(k, n, 2, torch.bfloat16) != other or other == planner  # per nproj
+    # the workspace covers the installed plan at any row count (two 64-row chunks above 64)
+    assert lib.mt_dense_workspace_bytes(128, k, n, 1) == 64 * 1024 + other.ksplit * 128 * n * 4
+    assert lib.mt_dense_workspace_bytes(1, k, n, 1) == 64 * 1024 + other.ksplit * 1 * n * 4
+    tuning.install_dense_plan(k, n, 1, torch.bfloat16, None)
+    assert tuning.dense_plan(k, n, 1, torch.bfloat16) == planner
+    assert lib.mt_dense_workspace_bytes(128, k, n, 1) == before
+
+
+@pytest.mark.parametrize("plan,message", [
+    (DensePlan(0), "ksplit must be in"),
+    (DensePlan(33), "ksplit must be in"),
+    (DensePlan(9), "equal-length splits"),    # 32 steps in runs of 4 make 8 splits, not 9
+    (DensePlan(16), "at least 4 K steps"),    # 32 steps in 16 splits of 2
+])
+def test_invalid_dense_plans_are_rejected(plan, message, clean_plans):
+    import torch
+
+    with pytest.raises(ValueError, match=message):
+        tuning.install_dense_plan(2048, 8192, 2, torch.bfloat16, plan)
