@@ -100,7 +100,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   __amdgpu_buffer_rsrc_t rw[NPROJ], rs[NPROJ], rb[NPROJ];
 #pragma unroll
   for (int pr = 0; pr < NPROJ; ++pr) {
-    rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * K * BITS / 8u);
+    rw[pr] = make_rsrc(p.w[pr], (uint32_t)N * (uint32_t)(K * BITS / 8));
     rs[pr] = make_rsrc(p.s[pr], (uint32_t)N * groups_per_row * 2u);
     rb[pr] = make_rsrc(p.b[pr], (uint32_t)N * groups_per_row * 2u);
   }

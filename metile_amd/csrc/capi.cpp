@@ -42,7 +42,7 @@ constexpr int kRowChunk = 32;  // rows per small-row dispatch
 // Every workspace starts with a fixed region of split-K arrival counters (one per 32-column
 // strip), shared by all shapes so that each counter is always found at the same place; every
 // call leaves the counters it used at zero. Partial sums follow the counter region.
-constexpr size_t kCounterBytes = 64 * 1024;
+constexpr size_t kCounterBytes = mt::kWorkspaceCounterBytes;
 constexpr int kMaxStrips = (int)(kCounterBytes / 4);
 
 // Split-K plan of the streaming kernels for one (K, N): about one workgroup per CU (splitting
@@ -831,6 +831,17 @@ int affine_swiglu_impl(const char* op, const void* x, const uint32_t* gate_w,
                  workspace_bytes, stream, layout);
 }
 
+int mlp_check_shape(const char* op, int M, int H, int I, int group_size, int bits, int dtype) {
+  const int st = check_affine(op, M, H, I, group_size, bits, dtype);
+  return st ? st : check_affine(op, M, I, H, group_size, bits, dtype);
+}
+
+int mlp_check_pointers(const char* op, const void* x, const void* y, const void* const p[9]) {
+  bool ok = x && y;
+  for (int i = 0; i < 9; ++i) ok = ok && p[i];
+  return ok ? MT_OK : fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null pointer");
+}
+
 int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
                     const void* gate_scales, const void* gate_biases, const uint32_t* up_w,
                     const void* up_scales, const void* up_biases, const uint32_t* down_w,
@@ -838,17 +849,16 @@ int affine_mlp_impl(const char* op, const void* x, const uint32_t* gate_w,
                     void* y, int M, int H, int I, int group_size, int bits, int dtype,
                     void* workspace, size_t workspace_bytes, void* stream, int up_layout,
                     int down_layout) {
-  int st = check_affine(op, M, H, I, group_size, bits, dtype);
-  if (st) return st;
-  st = check_affine(op, M, I, H, group_size, bits, dtype);
+  int st = mlp_check_shape(op, M, H, I, group_size, bits, dtype);
   if (st) return st;
   const size_t need = plan_mlp(M, H, I, group_size, bits).bytes;
   if (!workspace || workspace_bytes < need)
     return fail(MT_ERR_WORKSPACE, std::string(op) + ": workspace of " + std::to_string(need) +
                                       " bytes required, got " + std::to_string(workspace_bytes));
-  if (!x || !y || !gate_w || !gate_scales || !gate_biases || !up_w || !up_scales || !up_biases ||
-      !down_w || !down_scales || !down_biases)
-    return fail(MT_ERR_INVALID_ARGUMENT, std::string(op) + ": null pointer");
+  const void* const ptrs[9] = {gate_w, gate_scales, gate_biases, up_w, up_scales,
+                               up_biases, down_w, down_scales, down_biases};
+  st = mlp_check_pointers(op, x, y, ptrs);
+  if (st) return st;
   const MlpPlan mp = plan_mlp(M, H, I, group_size, bits);
   void* h = static_cast<char*>(workspace) + mp.hidden;
   st = affine_swiglu_impl(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases, h,
@@ -872,6 +882,18 @@ size_t affine_mlp_workspace(int M, int H, int I, int group_size, int bits) {
       check_affine("mt_affine_mlp", M, I, H, group_size, bits, MT_BF16))
     return 0;
   return plan_mlp(M, H, I, group_size, bits).bytes;
+}
+
+int affine_mlp_check(const char* op, const void* x, const uint32_t* gate_w,
+                     const void* gate_scales, const void* gate_biases, const uint32_t* up_w,
+                     const void* up_scales, const void* up_biases, const uint32_t* down_w,
+                     const void* down_scales, const void* down_biases, const void* y, int M,
+                     int H, int I, int group_size, int bits, int dtype) {
+  const int st = mlp_check_shape(op, M, H, I, group_size, bits, dtype);
+  if (st) return st;
+  const void* const ptrs[9] = {gate_w, gate_scales, gate_biases, up_w, up_scales,
+                               up_biases, down_w, down_scales, down_biases};
+  return mlp_check_pointers(op, x, y, ptrs);
 }
 
 int affine_mlp(const char* op, const void* x, const uint32_t* gate_w, const void* gate_scales,

@@ -9,9 +9,11 @@
 // on the first call there, and kept in g_scratch[]; kernels receive that pointer.
 //
 // Every call on a GPU shares that GPU's array, which keeps the last call's contents. The split-K
-// counters must start at zero: they are cleared once, by a fill kernel on the caller's stream at
-// set-up, and every call leaves them at zero again. Calls that overlap on one GPU (concurrent
-// streams, or a captured graph replayed while another call runs) race on the array.
+// counters must start at zero: the array has static storage, so it is zero when the library's
+// code object is loaded, and every call leaves the counters at zero again (no set-up kernel:
+// nothing is launched besides the MLP's own two kernels, under graph capture too). Calls that
+// overlap on one GPU (concurrent streams, or a captured graph replayed while another call runs)
+// race on the array.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -24,23 +26,18 @@
 namespace {
 
 constexpr size_t kScratchBytes = size_t(16) << 20;  // the stated maximum workspace
-constexpr size_t kCounterBytes = 64 * 1024;         // the workspace's leading counter region
+static_assert(kScratchBytes > mt::kWorkspaceCounterBytes, "room beyond the counter region");
 
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
-
-__global__ void clear_words(uint32_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
 
 constexpr int kMaxDevices = 64;
 std::mutex g_setup_mu;
 void* g_scratch[kMaxDevices];
 std::atomic<bool> g_ready[kMaxDevices];
 
-// The current device's scratch address, set up on its first use: the symbol's device address,
-// and the counter region cleared on `stream`.
-int device_scratch(void** out, hipStream_t stream) {
+// The current device's scratch address, taken from the symbol on the device's first use (no
+// stream work: the array needs no clearing).
+int device_scratch(void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess)
@@ -57,13 +54,6 @@ int device_scratch(void** out, hipStream_t stream) {
       if (e != hipSuccess || p == nullptr)
         return mt::set_last_error(
             MT_ERR_HIP, std::string("mt_affine_mlp_noalloc: hipGetSymbolAddress(scratch): ") +
-                            hipGetErrorString(e));
-      const int words = (int)(kCounterBytes / 4);
-      clear_words<<<(words + 255) / 256, 256, 0, stream>>>(static_cast<uint32_t*>(p), words);
-      e = hipGetLastError();
-      if (e != hipSuccess)
-        return mt::set_last_error(
-            MT_ERR_HIP, std::string("mt_affine_mlp_noalloc: clearing the scratch counters: ") +
                             hipGetErrorString(e));
       g_scratch[dev] = p;
       g_ready[dev].store(true, std::memory_order_release);
@@ -83,11 +73,12 @@ extern "C" int mt_affine_mlp_noalloc(const void* x, const uint32_t* gate_w, cons
                                      int H, int I, int group_size, int bits, int dtype,
                                      void* stream) {
   const char* op = "mt_affine_mlp_noalloc";
+  // Every argument check of the MLP first: nothing touches the device for a call it rejects.
+  int st = mt::affine_mlp_check(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales,
+                                up_biases, down_w, down_scales, down_biases, y, M, H, I,
+                                group_size, bits, dtype);
+  if (st) return st;
   const size_t need = mt::affine_mlp_workspace(M, H, I, group_size, bits);
-  if (need == 0)  // a shape the MLP rejects: let it report why (nothing is launched)
-    return mt::affine_mlp(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
-                          down_w, down_scales, down_biases, residual, y, M, H, I, group_size,
-                          bits, dtype, nullptr, 0, stream);
   if (need > kScratchBytes)
     return mt::set_last_error(
         MT_ERR_WORKSPACE, std::string(op) + ": this call needs " + std::to_string(need) +
@@ -95,7 +86,7 @@ extern "C" int mt_affine_mlp_noalloc(const void* x, const uint32_t* gate_w, cons
                               std::to_string(kScratchBytes) +
                               " (use mt_affine_mlp with a caller workspace)");
   void* ws = nullptr;
-  const int st = device_scratch(&ws, static_cast<hipStream_t>(stream));
+  st = device_scratch(&ws);
   if (st) return st;
   return mt::affine_mlp(op, x, gate_w, gate_scales, gate_biases, up_w, up_scales, up_biases,
                         down_w, down_scales, down_biases, residual, y, M, H, I, group_size, bits,

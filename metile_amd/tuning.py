@@ -304,6 +304,7 @@ def clear_plans() -> None:
         _decided.clear()
         _decided_layouts.clear()
         _resolved.clear()
+        _planner_seen.clear()
 
 
 # ---- timing and ranking -------------------------------------------------------------------------
@@ -393,6 +394,9 @@ _decided_layouts: dict[tuple, tuple] = {}
 # ensure_gemm_plan, with how: "measured" (tuned now), "cached" (a disk decision) or "planner"
 # (nothing decided: the library's own plan). Read by dispatches().
 _resolved: dict[tuple, str] = {}
+# The plan the library ran for a dispatch shape resolved with nothing decided, taken at that
+# dispatch's own row count (the planner plans from the rows, not from their bucket).
+_planner_seen: dict[tuple, object] = {}
 _identity: dict[int, dict] = {}
 _BASELINE = "planner"
 
@@ -657,6 +661,8 @@ def ensure_qmv_plans(values, weights, *, group_size, bits, autotune=True, retune
                         or torch.cuda.is_current_stream_capturing()):
                     out[rows] = None
                     _resolved.setdefault(mem, "planner")
+                    _planner_seen.setdefault(
+                        mem, qmv_plan(rows, k, n, group_size, bits, nproj, values.dtype))
                     continue  # not decided: the planner's plan, and measure another time
                 plan, record = _tune_qmv_dispatch(x[:rows], weights, group_size, bits, layout)
                 _write_decision(key, plan, {"op": "affine_qmv", **shape, **record})
@@ -928,6 +934,7 @@ def dispatches(op: str) -> tuple:
         resolved = dict(_resolved)
         decided = dict(_decided)
         layouts = dict(_decided_layouts)
+        seen = dict(_planner_seen)
     out = []
     for mem, source in resolved.items():
         if op == "matmul":
@@ -943,7 +950,8 @@ def dispatches(op: str) -> tuple:
         if mem[0] != "qmv" or mem[7] != (2 if op == "swiglu" else 1):
             continue
         _, device, bucket, k, n, group_size, bits, nproj, dtype = mem
-        plan = decided.get(mem) or qmv_plan(bucket, k, n, group_size, bits, nproj, dtype)
+        plan = (decided.get(mem) or seen.get(mem)
+                or qmv_plan(bucket, k, n, group_size, bits, nproj, dtype))
         layout = next((chosen for key, (_p, chosen) in layouts.items() if key[:9] == mem), None)
         out.append({"rows": bucket, "input_features": k, "output_features": n,
                     "dtype": str(dtype), "group_size": group_size, "bits": bits,

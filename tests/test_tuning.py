@@ -473,3 +473,24 @@ def test_invalid_dense_plans_are_rejected(plan, message, clean_plans):
 
     with pytest.raises(ValueError, match=message):
         tuning.install_dense_plan(2048, 8192, 2, torch.bfloat16, plan)
+
+
+def test_dispatches_report_the_plan_of_the_dispatch_rows_not_the_bucket(clean_plans, monkeypatch,
+                                                                       tmp_path):
+    """A shape resolved with nothing decided reports the plan the library runs at the
+    dispatch's own row count: the planner plans from the rows (two-strip workgroups from four
+    rows), which can differ within one row bucket (3 and 4 rows share bucket 4)."""
+    monkeypatch.setenv("METILE_AMD_CACHE_DIR", str(tmp_path))
+    monkeypatch.setattr(tuning, "_device_identity", lambda device: {"architecture": "cpu-test"})
+    bf = torch.bfloat16
+    k, n = 1536, 8960
+    assert tuning.qmv_plan(3, k, n, 64, 4, 2, bf) != tuning.qmv_plan(4, k, n, 64, 4, 2, bf)
+    x = torch.zeros(3, k, dtype=bf)
+    w = torch.zeros(n, k // 8, dtype=torch.int32)
+    s = torch.zeros(n, k // 64, dtype=bf)
+    assert tuning.ensure_qmv_plans(x, (w, s, s, w, s, s), group_size=64, bits=4,
+                                   autotune=False) == {3: None}
+    (d,) = tuning.dispatches("swiglu")
+    got = QmvPlan(d["kernel"], d["ksplit"], d["strips"], d["tiles"], d["order"])
+    assert (d["rows"], d["source"]) == (4, "planner")
+    assert got == tuning.qmv_plan(3, k, n, 64, 4, 2, bf)
