@@ -224,9 +224,18 @@ typedef struct mt_qmv_plan {
   int order;
 } mt_qmv_plan;
 
-/* How the prefill GEMM runs: output tiles of tile x tile (64 or 128) and K splits. */
+/* How the prefill GEMM runs: the kernel, its output tile (tile_m x tile_n) and the number of K
+ * splits. MT_GEMM_STAGED (v_mfma_f32_32x32x16, operands staged through registers into LDS):
+ * square tiles of 64 or 128, K split into equal lengths. MT_GEMM_RING (v_mfma_f32_16x16x32,
+ * activations and codes through three-stage LDS rings filled by buffer_load...lds): tiles of
+ * 128 x 64, 96, 160 or 192, N a multiple of 8, at most 8 splits of whole three-step lengths
+ * (steps of 64 along K). The reference's matmul plans race tile shapes the same way
+ * (MLXAffineMatmulConfig, metile/backends/mlx_affine.py:36-63). */
+typedef enum mt_gemm_kernel { MT_GEMM_STAGED = 0, MT_GEMM_RING = 1 } mt_gemm_kernel;
 typedef struct mt_gemm_plan {
-  int tile;
+  int kernel;
+  int tile_m;
+  int tile_n;
   int ksplit;
 } mt_gemm_plan;
 

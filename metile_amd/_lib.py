@@ -23,6 +23,8 @@ MT_F16 = 1
 MT_QMV_STAGED = 1
 MT_QMV_REGISTER = 2
 MT_QMV_GEMV = 3
+MT_GEMM_STAGED = 0
+MT_GEMM_RING = 1
 MT_LAYOUT_MLX = 0
 MT_LAYOUT_REPACKED = 1
 
@@ -37,7 +39,8 @@ class QmvPlan(ctypes.Structure):
 class GemmPlan(ctypes.Structure):
     """``mt_gemm_plan``."""
 
-    _fields_ = [("tile", ctypes.c_int), ("ksplit", ctypes.c_int)]
+    _fields_ = [("kernel", ctypes.c_int), ("tile_m", ctypes.c_int), ("tile_n", ctypes.c_int),
+                ("ksplit", ctypes.c_int)]
 
 
 class DensePlan(ctypes.Structure):

@@ -30,6 +30,11 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source extra flags. The ring GEMM keeps its MFMA results in ordinary VGPRs (the VALU
+# fix-up reads every one; in accumulation registers each read costs a copy).
+FILE_FLAGS = {"affine_gemm_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -46,6 +51,8 @@ def source_digest() -> str:
     order: the library reports it (``mt_source_digest``) so that persistent tuning decisions
     are keyed to the code they were measured on."""
     h = hashlib.sha256(" ".join(HIP_FLAGS).encode())
+    for name in sorted(FILE_FLAGS):
+        h.update((name + " " + " ".join(FILE_FLAGS[name])).encode())
     for path in sorted([*sources(), *CSRC.glob("*.h"), *INCLUDE.glob("*.h")],
                        key=lambda p: p.name):
         h.update(path.name.encode() + b"\0" + path.read_bytes() + b"\0")
@@ -54,7 +61,8 @@ def source_digest() -> str:
 
 def _compile(src: Path, digest: str) -> Path:
     obj = BUILD / (src.name + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, f"-DMT_SOURCE_DIGEST=\"{digest}\"", f"-I{CSRC}", f"-I{INCLUDE}",
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(src.name, []), f"-DMT_SOURCE_DIGEST=\"{digest}\"",
+           f"-I{CSRC}", f"-I{INCLUDE}",
            "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"

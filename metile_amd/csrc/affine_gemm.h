@@ -1,7 +1,8 @@
-// Host-visible launch interface of the prefill affine GEMM.
+// Host-visible launch interface of the prefill affine GEMM kernels.
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 namespace mt {
@@ -15,11 +16,36 @@ struct GemmParams {
   float* partial;      // [ksplit][M][N] split-K partial sums
   uint32_t* counters;  // one per output tile, zero between calls
   int M, K, N, G;
-  int tile;            // 2: 128 x 128 output tiles, 1: 64 x 64
+  int tile;            // register-staged kernel: 2: 128 x 128 output tiles, 1: 64 x 64
+  int tile_n;          // ring kernel: output tiles of 128 x tile_n (64, 96, 160 or 192)
   int ksplit;
   int steps_per_split;
+  int sb_words;        // ring kernel: dwords of scales (and of biases) staged per column
 };
 
+// Register-staged kernel (affine_gemm.hip).
 hipError_t launch_affine_gemm(const GemmParams& p, int dtype, hipStream_t stream);
+
+// Ring kernel (affine_gemm_ring.hip): G a power of two of 64 or more, N a multiple of 8,
+// steps_per_split a multiple of 3, ksplit <= kGemmMaxSplits, and the LDS of
+// gemm_ring_static_lds + gemm_ring_dynamic_lds within kGemmRingLdsBytes.
+hipError_t launch_affine_gemm_ring(const GemmParams& p, int dtype, hipStream_t stream);
+
+constexpr int kGemmMaxSplits = 8;
+constexpr size_t kGemmRingLdsBytes = 160 * 1024;  // LDS of a gfx950 CU
+
+// Static LDS of the ring kernel with output tiles 32 tn wide: three activation stages of 16 KiB
+// and three code stages of 1 KiB per 32 columns (plus a spare kilobyte when tn % 4 != 0).
+constexpr size_t gemm_ring_static_lds(int tn) {
+  return 3 * (size_t)(128 * 128) + 3 * (size_t)(tn * 1024 + (tn % 4 ? 1024 : 0)) + 16;
+}
+
+// Dynamic LDS: the staged scales and biases (sb_words dwords each per column), or the output
+// tile of 16-bit values, whichever is larger.
+constexpr size_t gemm_ring_dynamic_lds(int tn, int sb_words) {
+  const size_t sb = (size_t)2 * 32 * tn * sb_words * 4;
+  const size_t out = (size_t)128 * 32 * tn * 2;
+  return sb > out ? sb : out;
+}
 
 }  // namespace mt

@@ -1,0 +1,390 @@
+// Prefill affine quantized GEMM, ring kernel (gfx950): y[M, N] = x[M, K] @ dequantize(w_q)[N, K]^T
+// for many rows (reference: lower_affine_matmul, metile/compiler/affine_quantized.py:7-99, and its
+// dispatcher mlx_affine_matmul, metile/backends/mlx_affine.py:359-406). The plan picks it or the
+// register-staged kernel of affine_gemm.hip.
+//
+// A workgroup of four waves (2 x 2) computes a 128 x BN output tile (BN = 32 TN); each wave owns
+// 64 x 16 TN of it as 4 x TN tiles of v_mfma_f32_16x16x32. The K loop runs in 64-wide steps:
+//  * the step's activations (128 rows x 64) and codes (BN columns x 32 bytes) reach LDS through
+//    buffer_load...lds, three steps in flight in a ring of three stages, one barrier per step;
+//    no VGPR staging and no VALU on the way in. Each stage is its own LDS array, so the compiler
+//    sees that a step's reads do not touch the stage being filled and does not wait for it;
+//  * the scales and biases of the whole K range are staged once, before the loop;
+//  * a lane's B operand is two code words of one column read straight from the staged codes
+//    (k slices permuted alike in A and B: lane group g takes K 16 g .. 16 g + 15 of the step,
+//    8 per MFMA), unpacked to exact offset + q 16-bit floats;
+//  * an MFMA of the activations against -offset gives -offset * (row sum) in the output layout;
+//    each column block's chain starts from it, so the chain sums x * q exactly (the offset term
+//    cancels inside the fp32 accumulation, not in the output accumulator);
+//  * the group's affine terms are applied in fp32: acc += s t + b (-1/offset)(-offset X).
+// The MFMAs of column block c + 1 are issued ahead of the fix-up of block c, interleaved with it.
+// Output tiles leave through LDS as 16-byte stores; split-K partial sums and the last-arrival
+// reduction follow the same protocol as the register-staged kernel.
+#include "common.h"
+#include "affine_gemm.h"
+
+namespace mt {
+
+namespace {
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == kBF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+constexpr int kABytes = 128 * 128;  // one stage of activations: 128 rows x 64 K x 2 bytes
+
+// The 16-byte chunk c of LDS row r sits in slot c ^ swz(r): the A reads of 8 or 16 lanes
+// (consecutive rows, one chunk) hit distinct banks.
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// One step's loads: four 1 KiB activation loads per wave (rows 32 wave .. 32 wave + 31) and the
+// wave's share of the code loads (1 KiB = 32 columns each). Every wave issues the same number
+// of code loads, branch-free: a surplus one reads nothing (out of range) into the spare
+// kilobyte at the end of the code stage.
+template <int TN>
+__device__ __forceinline__ void ring_issue(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw,
+                                           const uint32_t* a_src, const uint32_t* c_src, int wave,
+                                           uint32_t st, bool ok, unsigned char* as,
+                                           unsigned char* bs) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(as + (32 * wave + 8 * d) * 128), 16,
+                                             oob_unless(ok, a_src[d] + st * 128u), 0, 0, 0);
+#pragma unroll
+  for (int i = 0; i < (TN + 3) / 4; ++i) {
+    const int d = wave + 4 * i;
+    const int dd = d < TN ? d : TN;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(bs + dd * 1024), 16,
+                                             oob_unless(ok && d < TN, c_src[i] + st * 32u), 0, 0,
+                                             0);
+  }
+}
+
+template <int DT, int TN>
+__global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams args) {
+  const GemmParams p = preload_args(args);
+  constexpr int BN = 32 * TN;
+  constexpr int kBBytes = BN * 32 + (TN % 4 ? 1024 : 0);
+  constexpr float kOff = CodeOffset<4, DT>::value;
+  constexpr uint32_t kNegOff2 = DT == kBF16 ? 0xC300C300u : 0xE400E400u;  // -offset, twice
+  // Ops a wave has in flight past the current step's at the start of a step: the next step's.
+  constexpr int kAhead = 4 + (TN + 3) / 4;
+  __shared__ __attribute__((aligned(1024))) unsigned char A0[kABytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char A1[kABytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char A2[kABytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char B0[kBBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char B1[kBBytes];
+  __shared__ __attribute__((aligned(1024))) unsigned char B2[kBBytes];
+  extern __shared__ __align__(16) unsigned char dyn[];  // scales and biases, then the output
+  auto a_stage = [&](auto sc) -> unsigned char* {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return A0;
+    else if constexpr (S == 1) return A1;
+    else return A2;
+  };
+  auto b_stage = [&](auto sc) -> unsigned char* {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return B0;
+    else if constexpr (S == 1) return B1;
+    else return B2;
+  };
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int i16 = lane & 15, g = lane >> 4;
+  const int M = p.M, K = p.K, N = p.N;
+  const int m0 = blockIdx.y * 128, n0 = blockIdx.x * BN;
+  const int steps = K >> 6;
+  const int s_beg = blockIdx.z * p.steps_per_split;
+  const int s_end = min(steps, s_beg + p.steps_per_split);
+  const int gshift = __builtin_ctz((unsigned)p.G);
+  const int gpr = K >> gshift;
+  const int g_beg = (s_beg * 64) >> gshift;
+  const uint32_t row_bytes = (uint32_t)K / 2u;
+  const int W = p.sb_words;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(p.x, (uint32_t)M * (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.w, (uint32_t)N * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(p.s, (uint32_t)N * (uint32_t)gpr * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(p.b, (uint32_t)N * (uint32_t)gpr * 2u);
+
+  // ---- scales and biases of the K range: dword q of [array][column][W] ----------------------
+  // Row q / W from a float reciprocal: (q + 1/2) / W stays 1 / (2 W) from an integer, far beyond
+  // the reciprocal's error for the sizes the host admits. A column's dwords start at the even
+  // element at or below its first group, so its groups start at element sh0 (0 or 1).
+  {
+    const int total = 2 * BN * W;
+    const float inv_w = __builtin_amdgcn_rcpf((float)W);
+    for (int d = wave; d * 64 < total; d += 4) {
+      const int q = d * 64 + lane;
+      const int rowq = (int)(((float)q + 0.5f) * inv_w);  // array * BN + column
+      const int wd = q - rowq * W;
+      const int arr = rowq >= BN;
+      const int n = n0 + rowq - arr * BN;
+      const uint32_t first = ((uint32_t)n * (uint32_t)gpr + (uint32_t)g_beg) & ~1u;
+      const uint32_t off = oob_unless(q < total && n < N, (first + 2u * wd) * 2u);
+      if (arr)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)(dyn + d * 256), 4, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(dyn + d * 256), 4, off, 0, 0, 0);
+    }
+  }
+
+  // Activations: load d of a wave fills LDS rows 32 wave + 8 d .. + 7, lane l the slot l % 8 of
+  // row l / 8, with the chunk that slot holds (rows past M read zero).
+  uint32_t a_src[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int r = 32 * wave + 8 * d + (lane >> 3);
+    const int c = (lane & 7) ^ swz(r);
+    a_src[d] = oob_unless(m0 + r < M, ((uint32_t)(m0 + r) * (uint32_t)K + 8u * c) * 2u);
+  }
+  // Codes: load d covers columns 32 d .. 32 d + 31, two lanes (16 bytes each) per column.
+  constexpr int kCodeLoads = (TN + 3) / 4;  // per wave and step
+  uint32_t c_src[kCodeLoads];
+#pragma unroll
+  for (int i = 0; i < kCodeLoads; ++i) {
+    const int n = n0 + 32 * (wave + 4 * i) + (lane >> 1);
+    c_src[i] = oob_unless(n < N, (uint32_t)n * row_bytes + 16u * (lane & 1));
+  }
+  auto issue = [&](int st, auto sc) {
+    ring_issue<TN>(rx, rw, a_src, c_src, wave, (uint32_t)st, st < s_end, a_stage(sc),
+                   b_stage(sc));
+  };
+  issue(s_beg, IntConst<0>{});
+  issue(s_beg + 1, IntConst<1>{});
+
+  f32x4 acc[4][TN];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < TN; ++c) acc[a][c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // Column of block c within the tile: lc0 + 16 c. Its staged scale row starts at parity sh0
+  // (16 c more columns of gpr groups each keep the parity of column lc0).
+  const int lc0 = wn * 16 * TN + i16;
+  const int sh0 = ((n0 + lc0) * gpr + g_beg) & 1;
+  const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(dyn);
+  const u32x4 negoff = (u32x4){kNegOff2, kNegOff2, kNegOff2, kNegOff2};
+  const f32x4 zero4 = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // Step st from stage S = (st - s_beg) % 3; the loads of step st + 2 go to stage (S + 2) % 3,
+  // which every wave finished reading in step st - 1, before this step's barrier.
+  auto step = [&](auto sc, int st) {
+    constexpr int S = decltype(sc)::value;
+    wait_vmcnt<kAhead>();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(st + 2, IntConst<(S + 2) % 3>{});
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char* as = a_stage(IntConst<S>{});
+    const unsigned char* bs = b_stage(IntConst<S>{});
+    u32x4 af[4][2];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int row = wm * 64 + 16 * a + i16;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        af[a][kk] = *reinterpret_cast<const u32x4*>(as + row * 128 +
+                                                    16 * ((2 * g + kk) ^ swz(row)));
+    }
+    u32x2 cw[TN];
+#pragma unroll
+    for (int c = 0; c < TN; ++c)
+      cw[c] = *reinterpret_cast<const u32x2*>(bs + (lc0 + 16 * c) * 32 + 8 * g);
+    const int gl = ((st * 64) >> gshift) - g_beg;
+    f32x4 tx[4], t[2][4];
+    u32x4 bw[2][2];
+    float sf[2], bq[2];
+    auto prep = [&](int c, int slot) {
+      bw[slot][0] = unpack_u4<DT>(cw[c].x);
+      bw[slot][1] = unpack_u4<DT>(cw[c].y);
+      const int e = (lc0 + 16 * c) * 2 * W + gl + sh0;
+      sf[slot] = act_to_f32<DT>(sb16[e]);
+      bq[slot] = act_to_f32<DT>(sb16[2 * BN * W + e]) * (-1.0f / kOff);  // exact: 2^-k
+    };
+    auto mm = [&](int slot) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        t[slot][a] = mfma16<DT>(af[a][0], bw[slot][0], tx[a]);
+        t[slot][a] = mfma16<DT>(af[a][1], bw[slot][1], t[slot][a]);
+      }
+    };
+    auto fix = [&](int c, int slot) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          acc[a][c][r] = __builtin_fmaf(sf[slot], t[slot][a][r], acc[a][c][r]);
+          acc[a][c][r] = __builtin_fmaf(bq[slot], tx[a][r], acc[a][c][r]);
+        }
+    };
+    prep(0, 0);
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      tx[a] = mfma16<DT>(af[a][0], negoff, zero4);
+      tx[a] = mfma16<DT>(af[a][1], negoff, tx[a]);
+    }
+    mm(0);
+    if (TN > 1) prep(1, 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c < TN; ++c) {
+      if (c + 1 < TN) mm((c + 1) & 1);
+      fix(c, c & 1);
+      if (c + 2 < TN) prep(c + 2, c & 1);
+      if (c + 1 < TN) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA,
+          __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // then six VALU
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // Steps in threes (the stages are compile-time): a split whose length is not a multiple of
+  // three runs one or two steps more over out-of-range loads (zero codes and activations; their
+  // scales are real), which add exact zeros.
+  for (int st = s_beg; st < s_end; st += 3) {
+    step(IntConst<0>{}, st);
+    step(IntConst<1>{}, st + 1);
+    step(IntConst<2>{}, st + 2);
+  }
+
+  if (p.ksplit == 1) {
+    // The output tile through LDS (the scale region, free once every wave is past its last
+    // step), then 16-byte row stores.
+    __syncthreads();
+    uint16_t* ot = reinterpret_cast<uint16_t*>(dyn);
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int c = 0; c < TN; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ot[(wm * 64 + 16 * a + 4 * g + r) * BN + lc0 + 16 * c] = f32_to_act<DT>(acc[a][c][r]);
+    __syncthreads();
+    constexpr int kChunks = 128 * BN / 8;
+    for (int q = tid; q < kChunks; q += 256) {
+      const int row = q / (BN / 8), c8 = (q - row * (BN / 8)) * 8;
+      if (m0 + row < M && n0 + c8 < N)  // N is a multiple of 8: a chunk is wholly inside
+        *reinterpret_cast<u32x4*>(p.y + (size_t)(m0 + row) * N + n0 + c8) =
+            *reinterpret_cast<const u32x4*>(ot + row * BN + c8);
+    }
+    return;
+  }
+
+  // ---- split-K: partials as device-coherent stores, the last workgroup of the tile sums -----
+  const __amdgpu_buffer_rsrc_t rp =
+      make_rsrc(p.partial, (uint32_t)p.ksplit * (uint32_t)M * (uint32_t)N * 4u);
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < TN; ++c)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + wm * 64 + 16 * a + 4 * g + r;
+        const int col = n0 + lc0 + 16 * c;
+        if (row < M && col < N)
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(acc[a][c][r]), rp,
+              (((uint32_t)blockIdx.z * M + row) * (uint32_t)N + col) * 4u, 0, kDeviceScope);
+      }
+  __shared__ int last_flag;
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    const unsigned prev =
+        __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = (prev == (unsigned)(p.ksplit - 1));
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  // Four outputs per thread at a time, every split's partial requested before any is added
+  // (in split order, so the sum does not depend on which workgroup finished last).
+  const size_t plane = (size_t)M * N;
+  for (int o0 = tid; o0 < 128 * BN; o0 += 4 * 256) {
+    float v[4][kGemmMaxSplits];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int o = o0 + 256 * u;
+      const int row = m0 + o / BN, col = n0 + o % BN;
+      const bool ok = o < 128 * BN && row < M && col < N;
+      const size_t base = ok ? (size_t)row * N + col : 0;
+#pragma unroll
+      for (int sp = 0; sp < kGemmMaxSplits; ++sp)
+        v[u][sp] = sp < p.ksplit ? __hip_atomic_load(p.partial + base + sp * plane,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int o = o0 + 256 * u;
+      const int row = m0 + o / BN, col = n0 + o % BN;
+      if (o < 128 * BN && row < M && col < N) {
+        float s = v[u][0];
+#pragma unroll
+        for (int sp = 1; sp < kGemmMaxSplits; ++sp)
+          if (sp < p.ksplit) s += v[u][sp];
+        p.y[(size_t)row * N + col] = f32_to_act<DT>(s);
+      }
+    }
+  }
+  if (tid == 0)
+    __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int DT, int TN>
+hipError_t launch_tn(const GemmParams& p, hipStream_t stream) {
+  constexpr int BN = 32 * TN;
+  const size_t dyn = gemm_ring_dynamic_lds(TN, p.sb_words);
+  // The kernel's dynamic LDS limit, raised once per instantiation to what the shapes the host
+  // admits may use.
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&affine_gemm_ring_kernel<DT, TN>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                          (int)(kGemmRingLdsBytes - gemm_ring_static_lds(TN)));
+  if (attr != hipSuccess) return attr;
+  const dim3 grid((p.N + BN - 1) / BN, (p.M + 127) / 128, p.ksplit);
+  affine_gemm_ring_kernel<DT, TN><<<grid, 256, dyn, stream>>>(p);
+  return hipGetLastError();
+}
+
+template <int DT>
+hipError_t launch_dt(const GemmParams& p, hipStream_t stream) {
+  switch (p.tile_n) {
+    case 64: return launch_tn<DT, 2>(p, stream);
+    case 96: return launch_tn<DT, 3>(p, stream);
+    case 160: return launch_tn<DT, 5>(p, stream);
+    case 192: return launch_tn<DT, 6>(p, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_affine_gemm_ring(const GemmParams& p, int dtype, hipStream_t stream) {
+  return dtype == kBF16 ? launch_dt<kBF16>(p, stream) : launch_dt<kF16>(p, stream);
+}
+
+}  // namespace mt

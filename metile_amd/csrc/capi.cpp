@@ -680,37 +680,133 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
   return MT_OK;
 }
 
-// Prefill GEMM plan: 128 x 128 tiles when they give at least about one workgroup per CU,
-// else 64 x 64 tiles; K is split when the tiles alone leave the chip underused.
+// Prefill GEMM plans. Kernel 0 (register-staged, affine_gemm.hip): square tiles of 64 or 128.
+// Kernel 1 (ring, affine_gemm_ring.hip): tiles of 128 x tile_n, tile_n 64, 96, 160 or 192, N a
+// multiple of 8, splits of a multiple of three K steps, at most kGemmMaxSplits of them.
 struct GemmPlan {
-  int tile;
+  int kernel;  // 0: register-staged, 1: ring
+  int tile;    // kernel 0: 2 (128 x 128) or 1 (64 x 64)
+  int tile_n;  // kernel 1
   int tiles;
   int ksplit;
   int steps_per_split;
+  int sb_words;  // kernel 1: scale (and bias) dwords staged per column
 };
-
-GemmPlan planner_gemm(int M, int K, int N) {
-  GemmPlan g;
-  const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
-  const int t64 = ((M + 63) / 64) * ((N + 63) / 64);
-  g.tile = t128 >= 200 ? 2 : 1;
-  g.tiles = g.tile == 2 ? t128 : t64;
-  // About three workgroups per CU in total, keeping at least 24 K steps per split (measured
-  // on MI355X at Qwen2.5-1.5B prefill shapes: up 1536x8960 best unsplit, down 8960x1536 best
-  // with four splits of 64 x 64 tiles).
-  const int steps = K / 64;
-  int ksplit = (768 + g.tiles / 2) / g.tiles;
-  const int max_split = steps / 24 > 0 ? steps / 24 : 1;
-  if (ksplit > max_split) ksplit = max_split;
-  if (ksplit < 1) ksplit = 1;
-  g.steps_per_split = (steps + ksplit - 1) / ksplit;
-  g.ksplit = (steps + g.steps_per_split - 1) / g.steps_per_split;
-  return g;
-}
 
 int gemm_tiles(int M, int N, int tile) {
   const int t = tile == 2 ? 128 : 64;
   return ((M + t - 1) / t) * ((N + t - 1) / t);
+}
+
+int ring_tiles(int M, int N, int tile_n) {
+  return ((M + 127) / 128) * ((N + tile_n - 1) / tile_n);
+}
+
+bool ring_tile_ok(int tile_n) {
+  return tile_n == 64 || tile_n == 96 || tile_n == 160 || tile_n == 192;
+}
+
+// Ring splits: equal lengths rounded up to whole loop iterations (three steps).
+Plan ring_split(int steps, int ksplit) {
+  Plan p{};
+  const int len = (steps + ksplit - 1) / ksplit;
+  p.steps_per_split = (len + 2) / 3 * 3;
+  p.ksplit = (steps + p.steps_per_split - 1) / p.steps_per_split;
+  return p;
+}
+
+// Scale dwords a ring split stages per column: the groups it spans at the smallest group size
+// (64; larger groups need fewer), one more for a start inside a dword.
+int ring_sb_words(int steps_per_split) { return steps_per_split / 2 + 1; }
+
+bool ring_lds_ok(int tile_n, int steps_per_split) {
+  const int tn = tile_n / 32;
+  return mt::gemm_ring_static_lds(tn) +
+             mt::gemm_ring_dynamic_lds(tn, ring_sb_words(steps_per_split)) <=
+         mt::kGemmRingLdsBytes;
+}
+
+GemmPlan make_ring(int M, int K, int N, int tile_n, int ksplit) {
+  GemmPlan g{};
+  g.kernel = 1;
+  g.tile_n = tile_n;
+  g.tiles = ring_tiles(M, N, tile_n);
+  const Plan p = ring_split(K / 64, ksplit);
+  g.ksplit = p.ksplit;
+  g.steps_per_split = p.steps_per_split;
+  g.sb_words = ring_sb_words(p.steps_per_split);
+  return g;
+}
+
+GemmPlan make_staged(int M, int K, int N, int tile, int ksplit) {
+  GemmPlan g{};
+  g.kernel = 0;
+  g.tile = tile;
+  g.tiles = gemm_tiles(M, N, tile);
+  const Plan p = split_plan(K / 64, ksplit);
+  g.ksplit = p.ksplit;
+  g.steps_per_split = p.steps_per_split;
+  return g;
+}
+
+// Why `q` cannot run the prefill GEMM at this shape for up to `M` rows ("" when it can); with a
+// split, one arrival counter per output tile.
+std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
+  const int steps = K / 64;
+  if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
+  if (q.kernel == 0) {
+    if (q.tile_m != q.tile_n || (q.tile_m != 64 && q.tile_m != 128))
+      return "kernel 0 takes square tiles of 64 or 128";
+    const Plan p = split_plan(steps, q.ksplit);
+    if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
+    if (q.ksplit > 1 && gemm_tiles(M, N, q.tile_m == 128 ? 2 : 1) > kMaxStrips)
+      return "too many output tiles to split K";
+    return "";
+  }
+  if (q.kernel != 1) return "kernel must be 0 (register-staged) or 1 (ring)";
+  if (q.tile_m != 128 || !ring_tile_ok(q.tile_n))
+    return "kernel 1 takes tiles of 128 x 64, 96, 160 or 192";
+  if (N % 8) return "kernel 1 needs N to be a multiple of 8";
+  if (q.ksplit > mt::kGemmMaxSplits) return "kernel 1 takes at most 8 K splits";
+  const Plan p = ring_split(steps, q.ksplit);
+  if (p.ksplit != q.ksplit)
+    return "ksplit does not divide K/64 into splits of whole three-step iterations";
+  if (!ring_lds_ok(q.tile_n, p.steps_per_split))
+    return "the split's scales and biases do not fit in LDS (split K further)";
+  if (q.ksplit > 1 && ring_tiles(M, N, q.tile_n) > kMaxStrips)
+    return "too many output tiles to split K";
+  return "";
+}
+
+// The planner (measured on MI355X at the Qwen2.5-1.5B prefill shapes, M = 512): the ring kernel
+// when N allows it, with 128 x 160 tiles unsplit when they give at least half a workgroup per
+// CU (up projection 1536 x 8960: 224 workgroups, 31.7 us against 42.5 us for the best
+// register-staged plan), else 128 x 64 tiles split K to about three workgroups per CU (down
+// projection 8960 x 1536: eight splits, 44.7 us against 47.7 us); the register-staged kernel
+// otherwise: 128 x 128 tiles when they give about one workgroup per CU, else 64 x 64, K split to
+// about three workgroups per CU keeping 24 steps per split.
+GemmPlan planner_gemm(int M, int K, int N) {
+  const int steps = K / 64;
+  if (N % 8 == 0) {
+    for (int tile_n : {160, 64}) {
+      const int tiles = ring_tiles(M, N, tile_n);
+      if (tile_n == 160 && tiles < 128) continue;
+      int ks = tile_n == 160 ? 1 : (768 + tiles / 2) / tiles;
+      ks = ks < 1 ? 1 : ks > mt::kGemmMaxSplits ? mt::kGemmMaxSplits : ks;
+      for (; ks <= mt::kGemmMaxSplits && ks <= steps; ++ks) {
+        const mt_gemm_plan q{1, 128, tile_n, ring_split(steps, ks).ksplit};
+        if (gemm_plan_problem(M, K, N, q).empty()) return make_ring(M, K, N, tile_n, q.ksplit);
+      }
+    }
+  }
+  const int t128 = gemm_tiles(M, N, 2), t64 = gemm_tiles(M, N, 1);
+  const int tile = t128 >= 200 ? 2 : 1;
+  const int tiles = tile == 2 ? t128 : t64;
+  int ksplit = (768 + tiles / 2) / tiles;
+  const int max_split = steps / 24 > 0 ? steps / 24 : 1;
+  if (ksplit > max_split) ksplit = max_split;
+  if (ksplit < 1) ksplit = 1;
+  return make_staged(M, K, N, tile, ksplit);
 }
 
 PlanKey gemm_key(int M, int K, int N, int group_size, int dtype) {
@@ -726,36 +822,19 @@ bool find_gemm_plan(const PlanKey& key, mt_gemm_plan* out) {
   return true;
 }
 
-// Why `q` cannot run the prefill GEMM at this shape for up to `M` rows ("" when it can): 64 x 64
-// (tile 64) or 128 x 128 (tile 128) output tiles, K split into equal-length splits, and with a
-// split one arrival counter per output tile.
-std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
-  const int steps = K / 64;
-  if (q.tile != 64 && q.tile != 128) return "tile must be 64 or 128";
-  if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
-  const Plan p = split_plan(steps, q.ksplit);
-  if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
-  if (q.ksplit > 1 && gemm_tiles(M, N, q.tile == 128 ? 2 : 1) > kMaxStrips)
-    return "too many output tiles to split K";
-  return "";
-}
-
 GemmPlan plan_gemm(int M, int K, int N, int group_size, int dtype) {
   mt_gemm_plan q;
   if (find_gemm_plan(gemm_key(M, K, N, group_size, dtype), &q)) {
-    GemmPlan g;
-    g.tile = q.tile == 128 ? 2 : 1;
-    g.tiles = gemm_tiles(M, N, g.tile);
-    const Plan p = split_plan(K / 64, q.ksplit);
-    g.ksplit = p.ksplit;
-    g.steps_per_split = p.steps_per_split;
-    return g;
+    if (q.kernel == 1) return make_ring(M, K, N, q.tile_n, q.ksplit);
+    return make_staged(M, K, N, q.tile_m == 128 ? 2 : 1, q.ksplit);
   }
   return planner_gemm(M, K, N);
 }
 
 mt_gemm_plan gemm_to_public(const GemmPlan& g) {
-  return mt_gemm_plan{g.tile == 2 ? 128 : 64, g.ksplit};
+  if (g.kernel == 1) return mt_gemm_plan{1, 128, g.tile_n, g.ksplit};
+  const int t = g.tile == 2 ? 128 : 64;
+  return mt_gemm_plan{0, t, t, g.ksplit};
 }
 
 std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
@@ -767,7 +846,17 @@ std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
       const Plan p = split_plan(steps, ks);
       if (p.ksplit == last) continue;
       last = p.ksplit;
-      const mt_gemm_plan q{tile, p.ksplit};
+      const mt_gemm_plan q{0, tile, tile, p.ksplit};
+      if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
+    }
+  }
+  for (int tile_n : {64, 96, 160, 192}) {
+    int last = 0;
+    for (int ks = 1; ks <= steps && ks <= mt::kGemmMaxSplits; ++ks) {
+      const Plan p = ring_split(steps, ks);
+      if (p.ksplit == last) continue;
+      last = p.ksplit;
+      const mt_gemm_plan q{1, 128, tile_n, p.ksplit};
       if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
     }
   }
@@ -1131,9 +1220,13 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
   p.N = N;
   p.G = group_size;
   p.tile = g.tile;
+  p.tile_n = g.tile_n;
   p.ksplit = g.ksplit;
   p.steps_per_split = g.steps_per_split;
-  const hipError_t e = mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));
+  p.sb_words = g.sb_words;
+  const hipError_t e =
+      g.kernel == 1 ? mt::launch_affine_gemm_ring(p, dtype, static_cast<hipStream_t>(stream))
+                    : mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "mt_affine_gemm");
   return MT_OK;
 }

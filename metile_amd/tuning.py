@@ -189,22 +189,30 @@ class QmvPlan:
         return self.strips // self.tiles * self.ksplit
 
 
+_GEMM_KERNELS = {_lib.MT_GEMM_STAGED: "staged", _lib.MT_GEMM_RING: "ring"}
+_GEMM_KERNEL_CODES = {v: k for k, v in _GEMM_KERNELS.items()}
+
+
 @dataclass(frozen=True)
 class GemmPlan:
-    """One prefill GEMM plan (``mt_gemm_plan``)."""
+    """One prefill GEMM plan (``mt_gemm_plan``): the kernel ("staged": square tiles of 64 or
+    128; "ring": tiles of 128 x 64, 96, 160 or 192), its tile and the K splits."""
 
-    tile: int
+    kernel: str
+    tile_m: int
+    tile_n: int
     ksplit: int
 
     def to_c(self) -> _lib.GemmPlan:
-        return _lib.GemmPlan(self.tile, self.ksplit)
+        return _lib.GemmPlan(_GEMM_KERNEL_CODES[self.kernel], self.tile_m, self.tile_n,
+                             self.ksplit)
 
     @classmethod
     def from_c(cls, p) -> "GemmPlan":
-        return cls(p.tile, p.ksplit)
+        return cls(_GEMM_KERNELS[p.kernel], p.tile_m, p.tile_n, p.ksplit)
 
     def workgroups(self, rows: int, n: int) -> int:
-        return -(-rows // self.tile) * -(-n // self.tile) * self.ksplit
+        return -(-rows // self.tile_m) * -(-n // self.tile_n) * self.ksplit
 
 
 @dataclass(frozen=True)
@@ -944,8 +952,8 @@ def dispatches(op: str) -> tuple:
             plan = decided.get(mem) or gemm_plan(bucket, k, n, group_size, dtype)
             out.append({"rows": bucket, "input_features": k, "output_features": n,
                         "dtype": str(dtype), "group_size": group_size, "bits": 4,
-                        "device": device, "tile": plan.tile, "ksplit": plan.ksplit,
-                        "source": source})
+                        "device": device, "kernel": plan.kernel, "tile_m": plan.tile_m,
+                        "tile_n": plan.tile_n, "ksplit": plan.ksplit, "source": source})
             continue
         if mem[0] != "qmv" or mem[7] != (2 if op == "swiglu" else 1):
             continue

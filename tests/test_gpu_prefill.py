@@ -78,3 +78,34 @@ def test_prefill_leading_dims():
     shaped = mt.mlx_affine_matmul(act_to_torch(x, "bf16").reshape(3, 4, 256), aw)
     assert tuple(shaped.shape) == (3, 4, 128)
     assert torch.equal(shaped.reshape(12, 128).view(torch.int16), flat.view(torch.int16))
+
+
+# Every plan the library lists at a ragged shape, in both 16-bit types and both group sizes:
+# partial output tiles in rows and columns for every tile width, split lengths that are not
+# whole three-step iterations (the ring kernel runs its padding steps over zeros), and splits
+# whose start falls inside a group of 128.
+@pytest.mark.parametrize("g,dtype", [(64, "f16"), (128, "bf16")])
+def test_every_prefill_plan_at_a_ragged_shape(g, dtype):
+    from metile_amd import tuning
+
+    m, k, n = 150, 1280, 480
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    w = O.make_affine_weight(n, k, 4, g, 21, 10, dtype)
+    x = O.make_activations(m, k, 21, dtype=dtype)
+    ref = reference(x, w, g, dtype)
+    wt = affine_to_torch(w, dtype)
+    xt = act_to_torch(x, dtype)
+    cands = tuning.gemm_plan_candidates(m, k, n, g)
+    assert {c.kernel for c in cands} == {"staged", "ring"}
+    try:
+        for plan in cands:
+            print(f"[prefill ragged {dtype} g{g}] plan {plan}", flush=True)
+            tuning.install_gemm_plan(m, k, n, g, tdt, plan)
+            got = torch_to_act(mt.affine_matmul(xt, *wt, group_size=g), dtype)
+            torch.cuda.synchronize()
+            err = O.tolerance_error(got, ref, dtype)
+            exact = float(np.mean(O.to_f32(got, dtype) ==
+                                  O.to_f32(O.from_f32(ref.astype(np.float32), dtype), dtype)))
+            assert err <= 2e-3 and exact >= (0.98 if dtype == "bf16" else 0.90), (plan, err, exact)
+    finally:
+        tuning.clear_plans()

@@ -339,16 +339,36 @@ def test_gemm_plans(clean_plans):
     lib = L.lib()
     m, k, n = 512, 8960, 1536
     planner = tuning.gemm_plan(m, k, n, 64, torch.bfloat16)
+    # the planner takes the ring kernel at config 4: 128 x 64 tiles, eight splits (18 steps)
+    assert planner == GemmPlan("ring", 128, 64, 8)
+    assert tuning.gemm_plan(512, 1536, 8960, 64, torch.bfloat16) == GemmPlan("ring", 128, 160, 1)
     cands = tuning.gemm_plan_candidates(m, k, n, 64)
-    assert planner in cands and {c.tile for c in cands} == {64, 128}
+    assert planner in cands
+    assert {(c.kernel, c.tile_m, c.tile_n) for c in cands} == {
+        ("staged", 64, 64), ("staged", 128, 128), ("ring", 128, 64), ("ring", 128, 96),
+        ("ring", 128, 160), ("ring", 128, 192)}
+    # ring splits are whole three-step lengths: 140 steps split 4 ways run 36 + 36 + 36 + 32
+    assert GemmPlan("ring", 128, 64, 4) in cands and GemmPlan("ring", 128, 64, 3) in cands
+    assert all(c.ksplit <= 8 for c in cands if c.kernel == "ring")
     before = lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4)
-    pick = next(c for c in cands if c.ksplit == 8 and c.tile == 64)
+    pick = next(c for c in cands if c.ksplit == 4 and c.kernel == "staged" and c.tile_m == 64)
     tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, pick)
     assert tuning.gemm_plan(300, k, n, 64, torch.bfloat16) == pick  # same bucket (512)
     assert tuning.gemm_plan(m, k, n, 64, torch.float16) == planner
+    # the workspace serves either dtype: bf16 takes 4 splits now, f16 the planner's 8
     assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == 64 * 1024 + 8 * m * n * 4
-    with pytest.raises(ValueError, match="tile must be 64 or 128"):
-        tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, GemmPlan(96, 1))
+    tuning.install_gemm_plan(m, k, n, 64, torch.float16, GemmPlan("ring", 128, 96, 2))
+    assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == 64 * 1024 + 4 * m * n * 4
+    for bad, why in ((GemmPlan("staged", 96, 96, 1), "kernel 0 takes square tiles"),
+                     (GemmPlan("staged", 128, 64, 1), "kernel 0 takes square tiles"),
+                     (GemmPlan("ring", 128, 128, 1), "kernel 1 takes tiles of 128 x"),
+                     (GemmPlan("ring", 64, 64, 1), "kernel 1 takes tiles of 128 x"),
+                     (GemmPlan("ring", 128, 64, 9), "at most 8 K splits")):
+        with pytest.raises(ValueError, match=why):
+            tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, bad)
+    # 24 steps in five splits: lengths of 6 (whole three-step iterations) give only four
+    with pytest.raises(ValueError, match="whole three-step iterations"):
+        tuning.install_gemm_plan(m, 1536, 8960, 64, torch.bfloat16, GemmPlan("ring", 128, 160, 5))
     tuning.clear_plans()
     assert tuning.gemm_plan(m, k, n, 64, torch.bfloat16) == planner
     assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == before
@@ -372,7 +392,7 @@ def test_dispatches_report_every_resolved_shape(clean_plans):
         tuning._decided[down1] = QmvPlan("gemv", 1, 768, 5, 1)
         tuning._decided_layouts[(*swiglu, ("repacked", "mlx"))] = (tuning._decided[swiglu],
                                                                    "mlx")
-        tuning._decided[gemm] = GemmPlan(128, 1)
+        tuning._decided[gemm] = GemmPlan("ring", 128, 160, 1)
 
     (sw,) = mt.mlx_affine_swiglu_dispatches()
     assert sw == {"rows": 1, "input_features": 1536, "output_features": 8960,
@@ -387,7 +407,8 @@ def test_dispatches_report_every_resolved_shape(clean_plans):
         planner.kernel, planner.ksplit, planner.strips, planner.tiles)
     assert qmv[0]["kernel"] == "gemv" and qmv[0]["strips"] == 768
     (mm,) = mt.mlx_affine_matmul_dispatches()
-    assert (mm["rows"], mm["tile"], mm["ksplit"], mm["source"]) == (512, 128, 1, "cached")
+    assert (mm["rows"], mm["kernel"], mm["tile_m"], mm["tile_n"], mm["ksplit"], mm["source"]) == (
+        512, "ring", 128, 160, 1, "cached")
     with pytest.raises(ValueError, match="op must be"):
         tuning.dispatches("dense")
     tuning.clear_plans()
