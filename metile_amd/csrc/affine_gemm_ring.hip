@@ -320,33 +320,43 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
   }
   __syncthreads();
   if (!last_flag) return;
-  // Four outputs per thread at a time, every split's partial requested before any is added
-  // (in split order, so the sum does not depend on which workgroup finished last).
-  const size_t plane = (size_t)M * N;
-  for (int o0 = tid; o0 < 128 * BN; o0 += 4 * 256) {
-    float v[4][kGemmMaxSplits];
+  // Four adjacent outputs per 16-byte load; four such chunks per thread at a time, every
+  // split's partial requested before any is added (in split order, so the sum does not depend
+  // on which workgroup finished last). The reduction is the last workgroup's alone, so its
+  // memory round trips are the kernel's tail: 16-byte device-coherent loads, all in flight.
+  constexpr int kChunks = 128 * BN / 4;
+  constexpr int kBatch = 4;
+  for (int q0 = tid; q0 < kChunks; q0 += kBatch * 256) {
+    u32x4 v[kBatch][kGemmMaxSplits];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int o = o0 + 256 * u;
-      const int row = m0 + o / BN, col = n0 + o % BN;
-      const bool ok = o < 128 * BN && row < M && col < N;
-      const size_t base = ok ? (size_t)row * N + col : 0;
+    for (int u = 0; u < kBatch; ++u) {
+      const int q = q0 + 256 * u;
+      const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
+      const bool ok = q < kChunks && row < M && col < N;  // N % 8 == 0: a chunk is whole
 #pragma unroll
       for (int sp = 0; sp < kGemmMaxSplits; ++sp)
-        v[u][sp] = sp < p.ksplit ? __hip_atomic_load(p.partial + base + sp * plane,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                 : 0.0f;
+        v[u][sp] = load16_device(
+            rp, oob_unless(ok && sp < p.ksplit,
+                           (((uint32_t)sp * M + row) * (uint32_t)N + col) * 4u));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int o = o0 + 256 * u;
-      const int row = m0 + o / BN, col = n0 + o % BN;
-      if (o < 128 * BN && row < M && col < N) {
-        float s = v[u][0];
+    for (int u = 0; u < kBatch; ++u) {
+      const int q = q0 + 256 * u;
+      const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
+      if (q < kChunks && row < M && col < N) {
+        f32x4 sum;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sum[e] = __uint_as_float(v[u][0][e]);
 #pragma unroll
         for (int sp = 1; sp < kGemmMaxSplits; ++sp)
-          if (sp < p.ksplit) s += v[u][sp];
-        p.y[(size_t)row * N + col] = f32_to_act<DT>(s);
+          if (sp < p.ksplit) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[e] += __uint_as_float(v[u][sp][e]);
+          }
+        u32x2 packed;
+        packed.x = (uint32_t)f32_to_act<DT>(sum[0]) | ((uint32_t)f32_to_act<DT>(sum[1]) << 16);
+        packed.y = (uint32_t)f32_to_act<DT>(sum[2]) | ((uint32_t)f32_to_act<DT>(sum[3]) << 16);
+        *reinterpret_cast<u32x2*>(p.y + (size_t)row * N + col) = packed;
       }
     }
   }
