@@ -166,8 +166,6 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     ring_issue<TN>(rx, rw, a_src, c_src, wave, (uint32_t)st, st < s_end, a_stage(sc),
                    b_stage(sc));
   };
-  issue(s_beg, IntConst<0>{});
-  issue(s_beg + 1, IntConst<1>{});
 
   f32x4 acc[4][TN];
 #pragma unroll
@@ -183,39 +181,57 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
   const u32x4 negoff = (u32x4){kNegOff2, kNegOff2, kNegOff2, kNegOff2};
   const f32x4 zero4 = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // Step st from stage S = (st - s_beg) % 3; the loads of step st + 2 go to stage (S + 2) % 3,
-  // which every wave finished reading in step st - 1, before this step's barrier.
-  auto step = [&](auto sc, int st) {
-    constexpr int S = decltype(sc)::value;
-    wait_vmcnt<kAhead>();
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    issue(st + 2, IntConst<(S + 2) % 3>{});
-    __builtin_amdgcn_sched_barrier(0);
-    const unsigned char* as = a_stage(IntConst<S>{});
-    const unsigned char* bs = b_stage(IntConst<S>{});
+  // A step's operands as a lane holds them: A fragments of its 4 row blocks (two K halves),
+  // two code words of each of its TN column blocks.
+  struct Frag {
     u32x4 af[4][2];
+    u32x2 cw[TN];
+  };
+  auto read_frags = [&](auto sc, Frag& f) {
+    const unsigned char* as = a_stage(sc);
+    const unsigned char* bs = b_stage(sc);
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
       const int row = wm * 64 + 16 * a + i16;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
-        af[a][kk] = *reinterpret_cast<const u32x4*>(as + row * 128 +
-                                                    16 * ((2 * g + kk) ^ swz(row)));
+        f.af[a][kk] = *reinterpret_cast<const u32x4*>(as + row * 128 +
+                                                      16 * ((2 * g + kk) ^ swz(row)));
     }
-    u32x2 cw[TN];
 #pragma unroll
     for (int c = 0; c < TN; ++c)
-      cw[c] = *reinterpret_cast<const u32x2*>(bs + (lc0 + 16 * c) * 32 + 8 * g);
+      f.cw[c] = *reinterpret_cast<const u32x2*>(bs + (lc0 + 16 * c) * 32 + 8 * g);
+  };
+  auto sync = [&]() {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Steps s_beg .. s_beg + 2 in flight, then the first step's operands.
+  issue(s_beg, IntConst<0>{});
+  issue(s_beg + 1, IntConst<1>{});
+  issue(s_beg + 2, IntConst<2>{});
+  wait_vmcnt<2 * kAhead>();
+  sync();
+  Frag f0, f1, f2;
+  read_frags(IntConst<0>{}, f0);
+
+  // Step st (stage S = (st - s_beg) % 3) computes from operands already in registers. Halfway
+  // through its column blocks it waits for step st + 1's loads (every wave's, at the barrier),
+  // refills stage S (every wave holds step st's operands by then) with step st + 3, and reads
+  // step st + 1's operands, whose LDS latency the remaining blocks hide.
+  auto step = [&](auto sc, int st, Frag& cur, Frag& nxt) {
+    constexpr int S = decltype(sc)::value;
+    constexpr int kMid = TN / 2;
     const int gl = ((st * 64) >> gshift) - g_beg;
     f32x4 tx[4], t[2][4];
     u32x4 bw[2][2];
     float sf[2], bq[2];
     auto prep = [&](int c, int slot) {
-      bw[slot][0] = unpack_u4<DT>(cw[c].x);
-      bw[slot][1] = unpack_u4<DT>(cw[c].y);
+      bw[slot][0] = unpack_u4<DT>(cur.cw[c].x);
+      bw[slot][1] = unpack_u4<DT>(cur.cw[c].y);
       const int e = (lc0 + 16 * c) * 2 * W + gl + sh0;
       sf[slot] = act_to_f32<DT>(sb16[e]);
       bq[slot] = act_to_f32<DT>(sb16[2 * BN * W + e]) * (-1.0f / kOff);  // exact: 2^-k
@@ -223,8 +239,8 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     auto mm = [&](int slot) {
 #pragma unroll
       for (int a = 0; a < 4; ++a) {
-        t[slot][a] = mfma16<DT>(af[a][0], bw[slot][0], tx[a]);
-        t[slot][a] = mfma16<DT>(af[a][1], bw[slot][1], t[slot][a]);
+        t[slot][a] = mfma16<DT>(cur.af[a][0], bw[slot][0], tx[a]);
+        t[slot][a] = mfma16<DT>(cur.af[a][1], bw[slot][1], t[slot][a]);
       }
     };
     auto fix = [&](int c, int slot) {
@@ -239,14 +255,21 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     prep(0, 0);
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      tx[a] = mfma16<DT>(af[a][0], negoff, zero4);
-      tx[a] = mfma16<DT>(af[a][1], negoff, tx[a]);
+      tx[a] = mfma16<DT>(cur.af[a][0], negoff, zero4);
+      tx[a] = mfma16<DT>(cur.af[a][1], negoff, tx[a]);
     }
     mm(0);
     if (TN > 1) prep(1, 1);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int c = 0; c < TN; ++c) {
+      if (c == kMid) {
+        wait_vmcnt<kAhead>();
+        sync();
+        issue(st + 3, IntConst<S>{});
+        read_frags(IntConst<(S + 1) % 3>{}, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       if (c + 1 < TN) mm((c + 1) & 1);
       fix(c, c & 1);
       if (c + 2 < TN) prep(c + 2, c & 1);
@@ -265,9 +288,9 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
   // three runs one or two steps more over out-of-range loads (zero codes and activations; their
   // scales are real), which add exact zeros.
   for (int st = s_beg; st < s_end; st += 3) {
-    step(IntConst<0>{}, st);
-    step(IntConst<1>{}, st + 1);
-    step(IntConst<2>{}, st + 2);
+    step(IntConst<0>{}, st, f0, f1);
+    step(IntConst<1>{}, st + 1, f1, f2);
+    step(IntConst<2>{}, st + 2, f2, f0);
   }
 
   if (p.ksplit == 1) {
