@@ -17,7 +17,7 @@ struct GemmParams {
   uint32_t* counters;  // one per output tile, zero between calls
   int M, K, N, G;
   int tile;            // register-staged kernel: 2: 128 x 128 output tiles, 1: 64 x 64
-  int tile_n;          // ring kernel: output tiles of 128 x tile_n (64, 96, 160 or 192)
+  int tile_n;          // ring kernel: output tiles of 128 x tile_n (64, 96, 128, 160, 192, 256)
   int ksplit;
   int steps_per_split;
   int sb_words;        // ring kernel: dwords of scales (and of biases) staged per column
@@ -34,17 +34,29 @@ hipError_t launch_affine_gemm_ring(const GemmParams& p, int dtype, hipStream_t s
 constexpr int kGemmMaxSplits = 8;
 constexpr size_t kGemmRingLdsBytes = 160 * 1024;  // LDS of a gfx950 CU
 
-// Static LDS of the ring kernel with output tiles 32 tn wide: three activation stages of 16 KiB
-// and three code stages of 1 KiB per 32 columns (plus a spare kilobyte when tn % 4 != 0).
-constexpr size_t gemm_ring_static_lds(int tn) {
-  return 3 * (size_t)(128 * 128) + 3 * (size_t)(tn * 1024 + (tn % 4 ? 1024 : 0)) + 16;
+// Workgroup waves of the ring kernel at a tile width: eight (four along N) for 128, 192 and 256,
+// else four.
+constexpr int gemm_ring_waves(int tile_n) {
+  return tile_n == 128 || tile_n == 192 || tile_n == 256 ? 8 : 4;
+}
+
+// One code stage of the ring kernel: 32 bytes per column, plus a spare kilobyte when the waves do
+// not share the 1 KiB code loads evenly.
+constexpr int gemm_ring_code_stage(int tile_n, int waves) {
+  return tile_n * 32 + ((tile_n / 32) % waves ? 1024 : 0);
+}
+
+// Static LDS of the ring kernel: three activation stages of 16 KiB and three code stages.
+constexpr size_t gemm_ring_static_lds(int tile_n) {
+  return 3 * (size_t)(128 * 128) +
+         3 * (size_t)gemm_ring_code_stage(tile_n, gemm_ring_waves(tile_n)) + 16;
 }
 
 // Dynamic LDS: the staged scales and biases (sb_words dwords each per column), or the output
 // tile of 16-bit values, whichever is larger.
-constexpr size_t gemm_ring_dynamic_lds(int tn, int sb_words) {
-  const size_t sb = (size_t)2 * 32 * tn * sb_words * 4;
-  const size_t out = (size_t)128 * 32 * tn * 2;
+constexpr size_t gemm_ring_dynamic_lds(int tile_n, int sb_words) {
+  const size_t sb = (size_t)2 * tile_n * sb_words * 4;
+  const size_t out = (size_t)128 * tile_n * 2;
   return sb > out ? sb : out;
 }
 

@@ -52,38 +52,45 @@ constexpr int kABytes = 128 * 128;  // one stage of activations: 128 rows x 64 K
 // (consecutive rows, one chunk) hit distinct banks.
 __device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
 
-// One step's loads: four 1 KiB activation loads per wave (rows 32 wave .. 32 wave + 31) and the
-// wave's share of the code loads (1 KiB = 32 columns each). Every wave issues the same number
-// of code loads, branch-free: a surplus one reads nothing (out of range) into the spare
-// kilobyte at the end of the code stage.
-template <int TN>
+// One step's loads by one of NW waves: 16 / NW activation loads of 1 KiB (rows
+// 128 / NW * wave ..) and the wave's share of the code loads (1 KiB = 32 columns each, load d
+// by wave d % NW). Every wave issues the same number of code loads, branch-free: a surplus one
+// reads nothing (out of range) into the spare kilobyte at the end of the code stage.
+template <int NW, int CODE_LOADS>
 __device__ __forceinline__ void ring_issue(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw,
                                            const uint32_t* a_src, const uint32_t* c_src, int wave,
                                            uint32_t st, bool ok, unsigned char* as,
                                            unsigned char* bs) {
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(as + (32 * wave + 8 * d) * 128), 16,
-                                             oob_unless(ok, a_src[d] + st * 128u), 0, 0, 0);
+  for (int d = 0; d < 16 / NW; ++d)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rx, (lds_ptr_t)(as + (128 / NW * wave + 8 * d) * 128), 16,
+        oob_unless(ok, a_src[d] + st * 128u), 0, 0, 0);
 #pragma unroll
-  for (int i = 0; i < (TN + 3) / 4; ++i) {
-    const int d = wave + 4 * i;
-    const int dd = d < TN ? d : TN;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(bs + dd * 1024), 16,
-                                             oob_unless(ok && d < TN, c_src[i] + st * 32u), 0, 0,
-                                             0);
+  for (int i = 0; i < (CODE_LOADS + NW - 1) / NW; ++i) {
+    const int d = wave + NW * i;
+    const int dd = d < CODE_LOADS ? d : CODE_LOADS;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rw, (lds_ptr_t)(bs + dd * 1024), 16,
+        oob_unless(ok && d < CODE_LOADS, c_src[i] + st * 32u), 0, 0, 0);
   }
 }
 
-template <int DT, int TN>
-__global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams args) {
+// TN column blocks of 16 per wave, WN waves along N (2 or 4) and two along M: tiles of
+// 128 x 16 TN WN, workgroups of 2 WN waves.
+template <int DT, int TN, int WN>
+__global__ __launch_bounds__(128 * WN) void affine_gemm_ring_kernel(const GemmParams args) {
   const GemmParams p = preload_args(args);
-  constexpr int BN = 32 * TN;
-  constexpr int kBBytes = BN * 32 + (TN % 4 ? 1024 : 0);
+  constexpr int NW = 2 * WN;
+  constexpr int kThreads = 64 * NW;
+  constexpr int BN = 16 * TN * WN;
+  constexpr int kCodeTotal = BN / 32;  // 1 KiB code loads per step
+  constexpr int kCodeLoads = (kCodeTotal + NW - 1) / NW;  // per wave and step
+  constexpr int kBBytes = gemm_ring_code_stage(BN, NW);
   constexpr float kOff = CodeOffset<4, DT>::value;
   constexpr uint32_t kNegOff2 = DT == kBF16 ? 0xC300C300u : 0xE400E400u;  // -offset, twice
   // Ops a wave has in flight past the current step's at the start of a step: the next step's.
-  constexpr int kAhead = 4 + (TN + 3) / 4;
+  constexpr int kAhead = 16 / NW + kCodeLoads;
   __shared__ __attribute__((aligned(1024))) unsigned char A0[kABytes];
   __shared__ __attribute__((aligned(1024))) unsigned char A1[kABytes];
   __shared__ __attribute__((aligned(1024))) unsigned char A2[kABytes];
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int i16 = lane & 15, g = lane >> 4;
   const int M = p.M, K = p.K, N = p.N;
   const int m0 = blockIdx.y * 128, n0 = blockIdx.x * BN;
@@ -130,7 +137,7 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
   {
     const int total = 2 * BN * W;
     const float inv_w = __builtin_amdgcn_rcpf((float)W);
-    for (int d = wave; d * 64 < total; d += 4) {
+    for (int d = wave; d * 64 < total; d += NW) {
       const int q = d * 64 + lane;
       const int rowq = (int)(((float)q + 0.5f) * inv_w);  // array * BN + column
       const int wd = q - rowq * W;
@@ -145,26 +152,25 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     }
   }
 
-  // Activations: load d of a wave fills LDS rows 32 wave + 8 d .. + 7, lane l the slot l % 8 of
-  // row l / 8, with the chunk that slot holds (rows past M read zero).
-  uint32_t a_src[4];
+  // Activations: load d of a wave fills LDS rows 128 / NW * wave + 8 d .. + 7, lane l the slot
+  // l % 8 of row l / 8, with the chunk that slot holds (rows past M read zero).
+  uint32_t a_src[16 / NW];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const int r = 32 * wave + 8 * d + (lane >> 3);
+  for (int d = 0; d < 16 / NW; ++d) {
+    const int r = 128 / NW * wave + 8 * d + (lane >> 3);
     const int c = (lane & 7) ^ swz(r);
     a_src[d] = oob_unless(m0 + r < M, ((uint32_t)(m0 + r) * (uint32_t)K + 8u * c) * 2u);
   }
   // Codes: load d covers columns 32 d .. 32 d + 31, two lanes (16 bytes each) per column.
-  constexpr int kCodeLoads = (TN + 3) / 4;  // per wave and step
   uint32_t c_src[kCodeLoads];
 #pragma unroll
   for (int i = 0; i < kCodeLoads; ++i) {
-    const int n = n0 + 32 * (wave + 4 * i) + (lane >> 1);
+    const int n = n0 + 32 * (wave + NW * i) + (lane >> 1);
     c_src[i] = oob_unless(n < N, (uint32_t)n * row_bytes + 16u * (lane & 1));
   }
   auto issue = [&](int st, auto sc) {
-    ring_issue<TN>(rx, rw, a_src, c_src, wave, (uint32_t)st, st < s_end, a_stage(sc),
-                   b_stage(sc));
+    ring_issue<NW, kCodeTotal>(rx, rw, a_src, c_src, wave, (uint32_t)st, st < s_end, a_stage(sc),
+                               b_stage(sc));
   };
 
   f32x4 acc[4][TN];
@@ -175,7 +181,7 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
 
   // Column of block c within the tile: lc0 + 16 c. Its staged scale row starts at parity sh0
   // (16 c more columns of gpr groups each keep the parity of column lc0).
-  const int lc0 = wn * 16 * TN + i16;
+  const int lc0 = wn * 16 * TN + i16;  // (also with four waves along N)
   const int sh0 = ((n0 + lc0) * gpr + g_beg) & 1;
   const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(dyn);
   const u32x4 negoff = (u32x4){kNegOff2, kNegOff2, kNegOff2, kNegOff2};
@@ -307,7 +313,7 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
           ot[(wm * 64 + 16 * a + 4 * g + r) * BN + lc0 + 16 * c] = f32_to_act<DT>(acc[a][c][r]);
     __syncthreads();
     constexpr int kChunks = 128 * BN / 8;
-    for (int q = tid; q < kChunks; q += 256) {
+    for (int q = tid; q < kChunks; q += kThreads) {
       const int row = q / (BN / 8), c8 = (q - row * (BN / 8)) * 8;
       if (m0 + row < M && n0 + c8 < N)  // N is a multiple of 8: a chunk is wholly inside
         *reinterpret_cast<u32x4*>(p.y + (size_t)(m0 + row) * N + n0 + c8) =
@@ -349,11 +355,11 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
   // memory round trips are the kernel's tail: 16-byte device-coherent loads, all in flight.
   constexpr int kChunks = 128 * BN / 4;
   constexpr int kBatch = 4;
-  for (int q0 = tid; q0 < kChunks; q0 += kBatch * 256) {
+  for (int q0 = tid; q0 < kChunks; q0 += kBatch * kThreads) {
     u32x4 v[kBatch][kGemmMaxSplits];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int q = q0 + 256 * u;
+      const int q = q0 + kThreads * u;
       const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
       const bool ok = q < kChunks && row < M && col < N;  // N % 8 == 0: a chunk is whole
 #pragma unroll
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int q = q0 + 256 * u;
+      const int q = q0 + kThreads * u;
       const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
       if (q < kChunks && row < M && col < N) {
         f32x4 sum;
@@ -387,29 +393,31 @@ __global__ __launch_bounds__(256) void affine_gemm_ring_kernel(const GemmParams 
     __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int DT, int TN>
+template <int DT, int TN, int WN>
 hipError_t launch_tn(const GemmParams& p, hipStream_t stream) {
-  constexpr int BN = 32 * TN;
-  const size_t dyn = gemm_ring_dynamic_lds(TN, p.sb_words);
+  constexpr int BN = 16 * TN * WN;
+  const size_t dyn = gemm_ring_dynamic_lds(BN, p.sb_words);
   // The kernel's dynamic LDS limit, raised once per instantiation to what the shapes the host
   // admits may use.
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&affine_gemm_ring_kernel<DT, TN>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&affine_gemm_ring_kernel<DT, TN, WN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                          (int)(kGemmRingLdsBytes - gemm_ring_static_lds(TN)));
+                          (int)(kGemmRingLdsBytes - gemm_ring_static_lds(BN)));
   if (attr != hipSuccess) return attr;
   const dim3 grid((p.N + BN - 1) / BN, (p.M + 127) / 128, p.ksplit);
-  affine_gemm_ring_kernel<DT, TN><<<grid, 256, dyn, stream>>>(p);
+  affine_gemm_ring_kernel<DT, TN, WN><<<grid, 128 * WN, dyn, stream>>>(p);
   return hipGetLastError();
 }
 
 template <int DT>
 hipError_t launch_dt(const GemmParams& p, hipStream_t stream) {
   switch (p.tile_n) {
-    case 64: return launch_tn<DT, 2>(p, stream);
-    case 96: return launch_tn<DT, 3>(p, stream);
-    case 160: return launch_tn<DT, 5>(p, stream);
-    case 192: return launch_tn<DT, 6>(p, stream);
+    case 64: return launch_tn<DT, 2, 2>(p, stream);
+    case 96: return launch_tn<DT, 3, 2>(p, stream);
+    case 128: return launch_tn<DT, 2, 4>(p, stream);
+    case 160: return launch_tn<DT, 5, 2>(p, stream);
+    case 192: return launch_tn<DT, 3, 4>(p, stream);
+    case 256: return launch_tn<DT, 4, 4>(p, stream);
   }
   return hipErrorInvalidValue;
 }

@@ -681,8 +681,9 @@ int run_dense(const char* op, int nproj, const void* x, const void* const w[2],
 }
 
 // Prefill GEMM plans. Kernel 0 (register-staged, affine_gemm.hip): square tiles of 64 or 128.
-// Kernel 1 (ring, affine_gemm_ring.hip): tiles of 128 x tile_n, tile_n 64, 96, 160 or 192, N a
-// multiple of 8, splits of a multiple of three K steps, at most kGemmMaxSplits of them.
+// Kernel 1 (ring, affine_gemm_ring.hip): tiles of 128 x tile_n, tile_n 64, 96, 128, 160, 192 or
+// 256 (workgroups of eight waves for 128, 192 and 256, else four), N a multiple of 8, splits of
+// a multiple of three K steps, at most kGemmMaxSplits of them.
 struct GemmPlan {
   int kernel;  // 0: register-staged, 1: ring
   int tile;    // kernel 0: 2 (128 x 128) or 1 (64 x 64)
@@ -703,7 +704,8 @@ int ring_tiles(int M, int N, int tile_n) {
 }
 
 bool ring_tile_ok(int tile_n) {
-  return tile_n == 64 || tile_n == 96 || tile_n == 160 || tile_n == 192;
+  return tile_n == 64 || tile_n == 96 || tile_n == 128 || tile_n == 160 || tile_n == 192 ||
+         tile_n == 256;
 }
 
 // Ring splits: equal lengths rounded up to whole loop iterations (three steps).
@@ -720,9 +722,8 @@ Plan ring_split(int steps, int ksplit) {
 int ring_sb_words(int steps_per_split) { return steps_per_split / 2 + 1; }
 
 bool ring_lds_ok(int tile_n, int steps_per_split) {
-  const int tn = tile_n / 32;
-  return mt::gemm_ring_static_lds(tn) +
-             mt::gemm_ring_dynamic_lds(tn, ring_sb_words(steps_per_split)) <=
+  return mt::gemm_ring_static_lds(tile_n) +
+             mt::gemm_ring_dynamic_lds(tile_n, ring_sb_words(steps_per_split)) <=
          mt::kGemmRingLdsBytes;
 }
 
@@ -765,7 +766,7 @@ std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
   }
   if (q.kernel != 1) return "kernel must be 0 (register-staged) or 1 (ring)";
   if (q.tile_m != 128 || !ring_tile_ok(q.tile_n))
-    return "kernel 1 takes tiles of 128 x 64, 96, 160 or 192";
+    return "kernel 1 takes tiles of 128 x 64, 96, 128, 160, 192 or 256";
   if (N % 8) return "kernel 1 needs N to be a multiple of 8";
   if (q.ksplit > mt::kGemmMaxSplits) return "kernel 1 takes at most 8 K splits";
   const Plan p = ring_split(steps, q.ksplit);
@@ -779,19 +780,20 @@ std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
 }
 
 // The planner (measured on MI355X at the Qwen2.5-1.5B prefill shapes, M = 512): the ring kernel
-// when N allows it, with 128 x 160 tiles unsplit when they give at least half a workgroup per
-// CU (up projection 1536 x 8960: 224 workgroups, 31.7 us against 42.5 us for the best
-// register-staged plan), else 128 x 64 tiles split K to about three workgroups per CU (down
-// projection 8960 x 1536: eight splits, 44.7 us against 47.7 us); the register-staged kernel
-// otherwise: 128 x 128 tiles when they give about one workgroup per CU, else 64 x 64, K split to
-// about three workgroups per CU keeping 24 steps per split.
+// when N allows it, with 128 x 192 tiles (eight-wave workgroups) unsplit when they give at
+// least half a workgroup per CU (up projection 1536 x 8960: 188 workgroups, 30.6 us; 128 x 160
+// four-wave tiles 31.3 us; the best register-staged plan 42.4 us), else 128 x 96 tiles with K
+// split to about one workgroup per CU (down projection 8960 x 1536: four splits, 36.4 us;
+// 128 x 64 in five splits 36.9 us; register-staged 47.0 us); the register-staged kernel
+// otherwise: 128 x 128 tiles when they give about one workgroup per CU, else 64 x 64, K split
+// to about three workgroups per CU keeping 24 steps per split.
 GemmPlan planner_gemm(int M, int K, int N) {
   const int steps = K / 64;
   if (N % 8 == 0) {
-    for (int tile_n : {160, 64}) {
+    for (int tile_n : {192, 96}) {
       const int tiles = ring_tiles(M, N, tile_n);
-      if (tile_n == 160 && tiles < 128) continue;
-      int ks = tile_n == 160 ? 1 : (768 + tiles / 2) / tiles;
+      if (tile_n == 192 && tiles < 128) continue;
+      int ks = tile_n == 192 ? 1 : (256 + tiles / 2) / tiles;
       ks = ks < 1 ? 1 : ks > mt::kGemmMaxSplits ? mt::kGemmMaxSplits : ks;
       for (; ks <= mt::kGemmMaxSplits && ks <= steps; ++ks) {
         const mt_gemm_plan q{1, 128, tile_n, ring_split(steps, ks).ksplit};
@@ -850,7 +852,7 @@ std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
       if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
     }
   }
-  for (int tile_n : {64, 96, 160, 192}) {
+  for (int tile_n : {64, 96, 128, 160, 192, 256}) {
     int last = 0;
     for (int ks = 1; ks <= steps && ks <= mt::kGemmMaxSplits; ++ks) {
       const Plan p = ring_split(steps, ks);

@@ -339,29 +339,31 @@ def test_gemm_plans(clean_plans):
     lib = L.lib()
     m, k, n = 512, 8960, 1536
     planner = tuning.gemm_plan(m, k, n, 64, torch.bfloat16)
-    # the planner takes the ring kernel at config 4: 128 x 64 tiles, eight splits (18 steps)
-    assert planner == GemmPlan("ring", 128, 64, 8)
-    assert tuning.gemm_plan(512, 1536, 8960, 64, torch.bfloat16) == GemmPlan("ring", 128, 160, 1)
+    # the planner takes the ring kernel at config 4: 128 x 96 tiles in four splits (36 steps)
+    # for the down projection, 128 x 192 tiles unsplit for the up projection
+    assert planner == GemmPlan("ring", 128, 96, 4)
+    assert tuning.gemm_plan(512, 1536, 8960, 64, torch.bfloat16) == GemmPlan("ring", 128, 192, 1)
     cands = tuning.gemm_plan_candidates(m, k, n, 64)
     assert planner in cands
     assert {(c.kernel, c.tile_m, c.tile_n) for c in cands} == {
         ("staged", 64, 64), ("staged", 128, 128), ("ring", 128, 64), ("ring", 128, 96),
-        ("ring", 128, 160), ("ring", 128, 192)}
+        ("ring", 128, 128), ("ring", 128, 160), ("ring", 128, 192), ("ring", 128, 256)}
     # ring splits are whole three-step lengths: 140 steps split 4 ways run 36 + 36 + 36 + 32
     assert GemmPlan("ring", 128, 64, 4) in cands and GemmPlan("ring", 128, 64, 3) in cands
     assert all(c.ksplit <= 8 for c in cands if c.kernel == "ring")
     before = lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4)
-    pick = next(c for c in cands if c.ksplit == 4 and c.kernel == "staged" and c.tile_m == 64)
+    pick = next(c for c in cands if c.ksplit == 8 and c.kernel == "staged" and c.tile_m == 64)
     tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, pick)
     assert tuning.gemm_plan(300, k, n, 64, torch.bfloat16) == pick  # same bucket (512)
     assert tuning.gemm_plan(m, k, n, 64, torch.float16) == planner
-    # the workspace serves either dtype: bf16 takes 4 splits now, f16 the planner's 8
+    # the workspace serves either dtype: bf16 takes 8 splits now, f16 the planner's 4
     assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == 64 * 1024 + 8 * m * n * 4
-    tuning.install_gemm_plan(m, k, n, 64, torch.float16, GemmPlan("ring", 128, 96, 2))
+    tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, GemmPlan("ring", 128, 96, 2))
     assert lib.mt_affine_gemm_workspace_bytes(m, k, n, 64, 4) == 64 * 1024 + 4 * m * n * 4
+    tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, pick)
     for bad, why in ((GemmPlan("staged", 96, 96, 1), "kernel 0 takes square tiles"),
                      (GemmPlan("staged", 128, 64, 1), "kernel 0 takes square tiles"),
-                     (GemmPlan("ring", 128, 128, 1), "kernel 1 takes tiles of 128 x"),
+                     (GemmPlan("ring", 128, 224, 1), "kernel 1 takes tiles of 128 x"),
                      (GemmPlan("ring", 64, 64, 1), "kernel 1 takes tiles of 128 x"),
                      (GemmPlan("ring", 128, 64, 9), "at most 8 K splits")):
         with pytest.raises(ValueError, match=why):
