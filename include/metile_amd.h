@@ -210,11 +210,16 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
  * 8 columns per group (8: one projection of up to 2 rows) and, when one pass of its lanes covers
  * K in whole rows of 16 lanes, several column groups per workgroup; `tiles` holds its waves per
  * workgroup (1 to 8) and `order` how workgroups take column groups (0: in index order; 1:
- * dealt out to the 8 XCDs in runs of adjacent groups). `order` is 0 for the other kernels. */
+ * dealt out to the 8 XCDs in runs of adjacent groups). The column-block kernel (up to 32 rows,
+ * groups of 64 or more) runs `strips` workgroups per K split, each a block of N / strips
+ * columns (at most 64, also when N is counted in the 4-column (4-bit) or 2-column (8-bit)
+ * units of the repacked layout) whose `tiles` waves (1 to 8) take consecutive runs of the
+ * split's K steps over every column of the block. `order` is 0 for every kernel but the GEMV. */
 typedef enum mt_qmv_kernel {
   MT_QMV_STAGED = 1,
   MT_QMV_REGISTER = 2,
-  MT_QMV_GEMV = 3
+  MT_QMV_GEMV = 3,
+  MT_QMV_BLOCK = 4
 } mt_qmv_kernel;
 typedef struct mt_qmv_plan {
   int kernel;

@@ -30,9 +30,11 @@ HIP_FLAGS = [
 ]
 
 
-# Per-source extra flags. The ring GEMM keeps its MFMA results in ordinary VGPRs (the VALU
-# fix-up reads every one; in accumulation registers each read costs a copy).
-FILE_FLAGS = {"affine_gemm_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source extra flags. The ring GEMM and the column-block kernel keep their MFMA results in
+# ordinary VGPRs (the VALU fix-up reads every one; in accumulation registers each read costs a
+# copy).
+FILE_FLAGS = {"affine_gemm_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+              "affine_qmv_block.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:

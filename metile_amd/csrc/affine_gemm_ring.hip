@@ -27,25 +27,6 @@ namespace mt {
 
 namespace {
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-template <int DT>
-__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
-  if constexpr (DT == kBF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
-}
-
 constexpr int kABytes = 128 * 128;  // one stage of activations: 128 rows x 64 K x 2 bytes
 
 // The 16-byte chunk c of LDS row r sits in slot c ^ swz(r): the A reads of 8 or 16 lanes

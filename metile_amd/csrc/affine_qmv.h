@@ -42,6 +42,8 @@ struct QmvParams {
   int gemv_groups_per_wave;  // GEMV kernel, whole groups in every wave: groups per wave
   int gemv_dealt;            // GEMV kernel: workgroups dealt out XCD by XCD (order 1: the grid
                              // rounded down to a multiple of 8; order 0: none)
+  int wave_steps;            // block kernel: K steps per wave (steps_per_split / waves, up)
+  int sb_words;              // block kernel: 32-bit words of one staged scale or bias row
 };
 
 // Step-major repack of MLX affine codes: the 8 * bits bytes of column n and K step t (codes
@@ -146,6 +148,43 @@ __host__ __device__ constexpr int affine_gemv_groups(int K, int bits, int waves)
 }
 hipError_t launch_affine_gemv(const QmvParams& p, int bits, int dtype, int nproj, int waves,
                               int cols, hipStream_t stream);
+
+// ---- column-block kernel (M <= 32, groups of 64 or more) ----------------------------------
+// A workgroup owns a block of at most kBlockMaxCols columns (block b = columns [b N / strips,
+// (b + 1) N / strips), in units of col_align) over the K range of its split (grid strips x
+// ksplit); its `waves` waves (1 to kBlockMaxWaves) take consecutive runs of wave_steps steps of
+// that range, each over every column of the block, with v_mfma_f32_16x16x32 (16-column tiles,
+// one or two 16-row tiles).
+constexpr int kBlockMaxWaves = 8;
+constexpr int kBlockMaxCols = 64;
+constexpr int kBlockMaxRows = 32;
+// Scale rows are staged for at most this many groups per split.
+constexpr int kBlockMaxGroups = 160;
+// Whether a wave's accumulators (tiles x projections x row tiles f32x4, and as many MFMA
+// results) leave room for its load ring in 256 registers.
+__host__ __device__ constexpr bool block_fits_registers(int tiles, int nproj, int row_tiles) {
+  return tiles * nproj * row_tiles <= 12;
+}
+// 16-column tiles of a block of `cols` columns.
+__host__ __device__ constexpr int block_tiles(int cols) { return (cols + 15) / 16; }
+// 32-bit words of one staged scale row covering `groups` groups (one more element for a row
+// that starts on an odd element, in whole words), rounded up to a power of two of at least 4.
+__host__ __device__ constexpr int block_sb_words(int groups) {
+  int w = 4;
+  while (w < (groups + 2) / 2) w *= 2;
+  return w;
+}
+// Dynamic LDS of one workgroup: the staged scale and bias rows, reused after the K loop by the
+// cross-wave reduction [waves][tiles][nproj][row tiles][64 lanes][4] (fp32).
+__host__ __device__ constexpr uint32_t block_lds_bytes(int waves, int tiles, int nproj,
+                                                       int row_tiles, int sb_words) {
+  const uint32_t sb = (uint32_t)(2 * nproj * 16 * tiles * sb_words) * 4u;
+  const uint32_t red = (uint32_t)(waves * tiles * nproj * row_tiles) * 1024u;
+  return sb > red ? sb : red;
+}
+constexpr uint32_t kBlockMaxLds = 160u * 1024u - 256u;
+hipError_t launch_affine_block(const QmvParams& p, int bits, int dtype, int nproj, int waves,
+                               int tiles, hipStream_t stream);
 
 
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* s, const uint16_t* b,

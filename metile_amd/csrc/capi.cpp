@@ -308,6 +308,27 @@ mt_qmv_plan to_public(const Plan& p) {
   return q;
 }
 
+// Widest block of a column-block plan of `strips` workgroups per split, over both code layouts
+// (repacked blocks start on whole 128-byte lines: units of 16 / bits columns).
+int block_max_cols(int N, int strips, int bits) {
+  const int align = 16 / bits;
+  const int plain = (N + strips - 1) / strips;
+  const int lined = (N / align + strips - 1) / strips * align;
+  return plain > lined ? plain : lined;
+}
+
+// Staged scale-row words of a column-block split of `steps_per_split` K steps: the groups it
+// spans, one more when it does not start on a group boundary.
+int block_sb_words_for(int steps_per_split, int group_size) {
+  const int per_group = group_size / 64;
+  return mt::block_sb_words((steps_per_split + per_group - 1) / per_group + 1);
+}
+
+int block_groups_for(int steps_per_split, int group_size) {
+  const int per_group = group_size / 64;
+  return (steps_per_split + per_group - 1) / per_group + 1;
+}
+
 // Why `q` cannot run dispatches of up to `rows` rows at this shape ("" when it can): the
 // register kernel covers 32-column strips of up to 32 rows and groups of 64 or more; the staged
 // kernel up to 16 rows, N / 32 to 2 N / 32 strips (16 to 32 columns each) in workgroups of one or
@@ -332,6 +353,29 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
     if (!mt::affine_gemv_fits(rows, nproj, N / q.strips / groups,
                               mt::affine_gemv_one_pass(K, bits, q.tiles)))
       return "the GEMV kernel does not hold this many columns and rows in registers";
+    return "";
+  }
+  if (q.kernel == MT_QMV_BLOCK) {
+    if (group_size < 64) return "the block kernel takes groups of 64 or more";
+    if (rows > mt::kBlockMaxRows) return "more rows than the block kernel takes";
+    if (q.order != 0) return "order is a GEMV plan field (0 for the other kernels)";
+    if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
+    const Plan p = split_plan(steps, q.ksplit);
+    if (p.ksplit != q.ksplit) return "ksplit does not divide K/64 into equal-length splits";
+    if (q.tiles < 1 || q.tiles > mt::kBlockMaxWaves || q.tiles > p.steps_per_split)
+      return "block tiles (waves per workgroup) must be in 1..min(8, K steps per split)";
+    if (q.strips < 1 || q.strips > kMaxStrips || q.strips > N / (16 / bits))
+      return "block strips must be in 1..N/(16/bits)";
+    const int cols = block_max_cols(N, q.strips, bits);
+    if (cols > mt::kBlockMaxCols) return "blocks wider than 64 columns";
+    if (!mt::block_fits_registers(mt::block_tiles(cols), nproj, rows <= 16 ? 1 : 2))
+      return "the block kernel does not hold this many columns and rows in registers";
+    if (block_groups_for(p.steps_per_split, group_size) > mt::kBlockMaxGroups)
+      return "too many groups per split";
+    const uint32_t lds = mt::block_lds_bytes(q.tiles, mt::block_tiles(cols), nproj,
+                                             rows <= 16 ? 1 : 2,
+                                             block_sb_words_for(p.steps_per_split, group_size));
+    if (lds > mt::kBlockMaxLds) return "the block kernel's LDS does not hold this plan";
     return "";
   }
   if (q.kernel != MT_QMV_STAGED && q.kernel != MT_QMV_REGISTER) return "unknown kernel";
@@ -428,6 +472,23 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
         const mt_qmv_plan g{MT_QMV_GEMV, 1, N / per_wg, w, order};
         if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
       }
+  // Column blocks: one or two workgroups per CU, or blocks of 16 or 32 columns; 4 or 8 waves;
+  // K unsplit or in 4 splits.
+  {
+    const int kCus = device_cus();
+    std::vector<int> strips;
+    for (int s : {kCus, 2 * kCus, N / 16, N / 32})
+      if (s >= 1 && std::find(strips.begin(), strips.end(), s) == strips.end()) strips.push_back(s);
+    for (int ks : {1, 4}) {
+      const Plan p = split_plan(steps, ks);
+      if (p.ksplit != ks) continue;
+      for (int s : strips)
+        for (int w : {8, 4}) {
+          const mt_qmv_plan b{MT_QMV_BLOCK, ks, s, w, 0};
+          if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, b).empty()) out.push_back(b);
+        }
+    }
+  }
   return out;
 }
 
@@ -548,8 +609,16 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
     const int units = N / p.col_align;
     p.strip_cols = units % p.strips == 0 ? units / p.strips * p.col_align : 0;
     p.groups_per_row = K / group_size;
+    if (plan.kernel == MT_QMV_BLOCK) {
+      p.wave_steps = (plan.steps_per_split + plan.tiles - 1) / plan.tiles;
+      p.sb_words = block_sb_words_for(plan.steps_per_split, group_size);
+    }
     hipError_t e;
-    if (plan.kernel == MT_QMV_GEMV)
+    if (plan.kernel == MT_QMV_BLOCK)
+      e = mt::launch_affine_block(
+          p, bits, dtype, nproj, plan.tiles,
+          mt::block_tiles((units + plan.strips - 1) / plan.strips * p.col_align), hs);
+    else if (plan.kernel == MT_QMV_GEMV)
       e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles,
                                  N / plan.strips / mt::affine_gemv_groups(K, bits, plan.tiles),
                                  hs);

@@ -125,6 +125,29 @@ __device__ __forceinline__ constexpr int mfma32_row(int r, int h) {
   return 8 * (r / 4) + 4 * h + (r % 4);
 }
 
+// ---- MFMA 16x16x32 (fp32 accumulate) -----------------------------------------------------
+// Lane l supplies A[i = l%16][k = 8*(l/16) + 0..7] and B[k = 8*(l/16) + 0..7][j = l%16]; the
+// result element (i, j) lives in lane j + 16*(i/4), register i%4.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == kBF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// LDS address space, for buffer_load...lds destinations.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
 // ---- code -> 16-bit float unpack (exact) -------------------------------------------------
 // A 4-bit code q is written into the low mantissa bits of a 16-bit float whose exponent makes
 // the mantissa step exactly 1: bf16 0x4300|q == 128 + q, f16 0x6400|q == 1024 + q. 8-bit

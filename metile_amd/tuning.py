@@ -68,7 +68,7 @@ CACHE_FILE = "affine-plans-v2.jsonl"
 _LAYOUT_MLX, _LAYOUT_REPACKED = 0, 1
 _LAYOUT_NAMES = {_LAYOUT_MLX: "mlx", _LAYOUT_REPACKED: "repacked"}
 _KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register",
-            _lib.MT_QMV_GEMV: "gemv"}
+            _lib.MT_QMV_GEMV: "gemv", _lib.MT_QMV_BLOCK: "block"}
 _KERNEL_CODES = {v: k for k, v in _KERNELS.items()}
 
 
@@ -168,10 +168,10 @@ def row_bucket(rows: int) -> int:
 class QmvPlan:
     """One small-row dispatch plan (``mt_qmv_plan``)."""
 
-    kernel: str  # "staged", "register" or "gemv"
+    kernel: str  # "staged", "register", "gemv" or "block"
     ksplit: int
     strips: int
-    tiles: int = 1  # staged: strips per workgroup; gemv: waves per workgroup
+    tiles: int = 1  # staged: strips per workgroup; gemv and block: waves per workgroup
     order: int = 0  # gemv: 0 index order, 1 column groups dealt out XCD by XCD
 
     def to_c(self) -> _lib.QmvPlan:
@@ -186,6 +186,8 @@ class QmvPlan:
     def workgroups(self) -> int:
         if self.kernel == "gemv":
             return self.strips
+        if self.kernel == "block":
+            return self.strips * self.ksplit
         return self.strips // self.tiles * self.ksplit
 
 

@@ -224,12 +224,21 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
         sorted((n // (c * groups(w)), w, o) for c in (2, 4, 8) for w in waves for o in (0, 1)
                if fits(c, w) and n % (c * groups(w)) == 0)
         if bucket <= 4 else [])
+    # column blocks: one or two workgroups per CU (256 CUs on the host, with no device), or
+    # blocks of 16 or 32 columns, at most 64 wide in either code layout; 4 or 8 waves; K unsplit
+    # or in 4 equal splits; groups of 64 or more
+    align = 16 // bits
     for c in cands:
-        assert c.kernel in ("staged", "register", "gemv")
+        assert c.kernel in ("staged", "register", "gemv", "block")
         if c.kernel == "register":
             assert g != 32 and c.strips == n // 32 and c.tiles == 1
         elif c.kernel == "gemv":
             assert c.ksplit == 1 and c.workgroups == c.strips
+        elif c.kernel == "block":
+            assert g >= 64 and rows <= 32 and c.order == 0
+            assert c.ksplit in (1, 4) and c.tiles in (4, 8)
+            assert c.strips in (256, 512, n // 16, n // 32)
+            assert max(-(-n // c.strips), -(-(n // align) // c.strips) * align) <= 64
         else:
             assert rows <= (16 if g == 32 else 32)
             assert n // 32 <= c.strips <= 2 * (n // 32) and c.strips % c.tiles == 0
