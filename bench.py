@@ -258,6 +258,9 @@ def kernel_label(k, n, nproj):
     if plan.kernel == "staged":
         return (f"affine_qmv_lds_kernel<{BITS}, 0, 8, {nproj}, ...> "
                 f"({plan.strips} strips, {plan.ksplit} K splits)")
+    if plan.kernel == "block":
+        return (f"affine_block_kernel<{BITS}, 0, {nproj}, 1, {-(-(-(-n // plan.strips)) // 16)}> "
+                f"({plan.strips} blocks x {plan.ksplit} K splits, {plan.tiles} waves each)")
     return f"affine_qmv_kernel<{BITS}, 0, ..., {nproj}, ...> ({plan.ksplit} K splits)"
 
 
