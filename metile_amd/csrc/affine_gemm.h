@@ -13,7 +13,8 @@ struct GemmParams {
   const uint16_t* s;   // [N, K/G] scales
   const uint16_t* b;   // [N, K/G] biases
   uint16_t* y;         // [M, N] output
-  float* partial;      // [ksplit][M][N] split-K partial sums
+  float* partial;      // split-K partial sums: [ksplit][M][N] (register-staged kernel) or
+                       // [ksplit][tile][128 x tile_n] in register layout (ring kernel)
   uint32_t* counters;  // one per output tile, zero between calls
   int M, K, N, G;
   int tile;            // register-staged kernel: 2: 128 x 128 output tiles, 1: 64 x 64

@@ -18,8 +18,8 @@
 //    cancels inside the fp32 accumulation, not in the output accumulator);
 //  * the group's affine terms are applied in fp32: acc += s t + b (-1/offset)(-offset X).
 // The MFMAs of column block c + 1 are issued ahead of the fix-up of block c, interleaved with it.
-// Output tiles leave through LDS as 16-byte stores; split-K partial sums and the last-arrival
-// reduction follow the same protocol as the register-staged kernel.
+// Output tiles leave through LDS as 16-byte stores. With K split, the last workgroup of a tile
+// to arrive adds the other splits' accumulators, stored in register layout, to its own.
 #include "common.h"
 #include "affine_gemm.h"
 
@@ -280,98 +280,92 @@ __global__ __launch_bounds__(128 * WN) void affine_gemm_ring_kernel(const GemmPa
     step(IntConst<2>{}, st + 2, f2, f0);
   }
 
-  if (p.ksplit == 1) {
-    // The output tile through LDS (the scale region, free once every wave is past its last
-    // step), then 16-byte row stores.
-    __syncthreads();
-    uint16_t* ot = reinterpret_cast<uint16_t*>(dyn);
+  if (p.ksplit > 1) {
+    // ---- split K: each workgroup leaves its accumulators as they lie in its registers
+    // (thread t's f32x4 j at 16 (j kThreads + t) bytes of its part: each wave store 1 KiB
+    // contiguous, device-coherent); the last to arrive adds the other splits' parts to its own
+    // in split order (so the sum does not depend on which arrived last) and stores the tile.
+    // Parts are [split][tile][128 BN] fp32.
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int tiles = gridDim.x * gridDim.y;
+    const int split = blockIdx.z, parts = p.ksplit;
+    constexpr uint32_t kPartBytes = 128u * BN * 4u;
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc(p.partial, (uint32_t)parts * (uint32_t)tiles * kPartBytes);
+    auto part_off = [&](int sp, int j) {
+      return ((uint32_t)sp * tiles + tile) * kPartBytes + ((uint32_t)j * kThreads + tid) * 16u;
+    };
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
       for (int c = 0; c < TN; ++c)
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          ot[(wm * 64 + 16 * a + 4 * g + r) * BN + lc0 + 16 * c] = f32_to_act<DT>(acc[a][c][r]);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[a][c]), rp,
+                                               part_off(split, a * TN + c), 0, kDeviceScope);
+    __shared__ int last_flag;
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    constexpr int kChunks = 128 * BN / 8;
-    for (int q = tid; q < kChunks; q += kThreads) {
-      const int row = q / (BN / 8), c8 = (q - row * (BN / 8)) * 8;
-      if (m0 + row < M && n0 + c8 < N)  // N is a multiple of 8: a chunk is wholly inside
-        *reinterpret_cast<u32x4*>(p.y + (size_t)(m0 + row) * N + n0 + c8) =
-            *reinterpret_cast<const u32x4*>(ot + row * BN + c8);
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      last_flag = (prev == (unsigned)(parts - 1));
     }
-    return;
+    __syncthreads();
+    if (!last_flag) return;
+    if (tid == 0)
+      __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Two parts in flight at a time (one for the widest tiles, for registers); the own part
+    // from registers.
+    constexpr int kBufs = TN >= 4 ? 1 : 2;
+    f32x4 tot[4][TN];
+    u32x4 v[kBufs][4][TN];
+    auto fetch = [&](int sp, u32x4 (&d)[4][TN]) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < TN; ++c)
+          d[a][c] = load16_device(
+              rp, oob_unless(sp < parts && sp != split, part_off(sp, a * TN + c)));
+    };
+    if (kBufs == 2) fetch(0, v[0]);
+#pragma unroll
+    for (int sp = 0; sp < kGemmMaxSplits; ++sp) {
+      if (sp >= parts) break;
+      if (kBufs == 1) fetch(sp, v[0]);
+      else if (sp + 1 < parts) fetch(sp + 1, v[(sp + 1) % kBufs]);
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int c = 0; c < TN; ++c) {
+          const f32x4 x =
+              sp == split ? acc[a][c] : __builtin_bit_cast(f32x4, v[sp % kBufs][a][c]);
+          tot[a][c] = sp == 0 ? x : tot[a][c] + x;
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int c = 0; c < TN; ++c) acc[a][c] = tot[a][c];
   }
 
-  // ---- split-K: partials as device-coherent stores, the last workgroup of the tile sums -----
-  const __amdgpu_buffer_rsrc_t rp =
-      make_rsrc(p.partial, (uint32_t)p.ksplit * (uint32_t)M * (uint32_t)N * 4u);
+  // ---- the output tile through LDS (the scale region, free once every wave is past its last
+  // step), then 16-byte row stores ------------------------------------------------------------
+  __syncthreads();
+  uint16_t* ot = reinterpret_cast<uint16_t*>(dyn);
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < TN; ++c)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * 64 + 16 * a + 4 * g + r;
-        const int col = n0 + lc0 + 16 * c;
-        if (row < M && col < N)
-          __builtin_amdgcn_raw_buffer_store_b32(
-              __float_as_uint(acc[a][c][r]), rp,
-              (((uint32_t)blockIdx.z * M + row) * (uint32_t)N + col) * 4u, 0, kDeviceScope);
-      }
-  __shared__ int last_flag;
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      for (int r = 0; r < 4; ++r)
+        ot[(wm * 64 + 16 * a + 4 * g + r) * BN + lc0 + 16 * c] = f32_to_act<DT>(acc[a][c][r]);
   __syncthreads();
-  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-  if (tid == 0) {
-    const unsigned prev =
-        __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_flag = (prev == (unsigned)(p.ksplit - 1));
+  constexpr int kChunks = 128 * BN / 8;
+  for (int q = tid; q < kChunks; q += kThreads) {
+    const int row = q / (BN / 8), c8 = (q - row * (BN / 8)) * 8;
+    if (m0 + row < M && n0 + c8 < N)  // N is a multiple of 8: a chunk is wholly inside
+      *reinterpret_cast<u32x4*>(p.y + (size_t)(m0 + row) * N + n0 + c8) =
+          *reinterpret_cast<const u32x4*>(ot + row * BN + c8);
   }
-  __syncthreads();
-  if (!last_flag) return;
-  // Four adjacent outputs per 16-byte load; four such chunks per thread at a time, every
-  // split's partial requested before any is added (in split order, so the sum does not depend
-  // on which workgroup finished last). The reduction is the last workgroup's alone, so its
-  // memory round trips are the kernel's tail: 16-byte device-coherent loads, all in flight.
-  constexpr int kChunks = 128 * BN / 4;
-  constexpr int kBatch = 4;
-  for (int q0 = tid; q0 < kChunks; q0 += kBatch * kThreads) {
-    u32x4 v[kBatch][kGemmMaxSplits];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int q = q0 + kThreads * u;
-      const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
-      const bool ok = q < kChunks && row < M && col < N;  // N % 8 == 0: a chunk is whole
-#pragma unroll
-      for (int sp = 0; sp < kGemmMaxSplits; ++sp)
-        v[u][sp] = load16_device(
-            rp, oob_unless(ok && sp < p.ksplit,
-                           (((uint32_t)sp * M + row) * (uint32_t)N + col) * 4u));
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int q = q0 + kThreads * u;
-      const int row = m0 + q / (BN / 4), col = n0 + (q % (BN / 4)) * 4;
-      if (q < kChunks && row < M && col < N) {
-        f32x4 sum;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) sum[e] = __uint_as_float(v[u][0][e]);
-#pragma unroll
-        for (int sp = 1; sp < kGemmMaxSplits; ++sp)
-          if (sp < p.ksplit) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sum[e] += __uint_as_float(v[u][sp][e]);
-          }
-        u32x2 packed;
-        packed.x = (uint32_t)f32_to_act<DT>(sum[0]) | ((uint32_t)f32_to_act<DT>(sum[1]) << 16);
-        packed.y = (uint32_t)f32_to_act<DT>(sum[2]) | ((uint32_t)f32_to_act<DT>(sum[3]) << 16);
-        *reinterpret_cast<u32x2*>(p.y + (size_t)row * N + col) = packed;
-      }
-    }
-  }
-  if (tid == 0)
-    __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int DT, int TN, int WN>

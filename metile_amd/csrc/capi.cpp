@@ -845,6 +845,9 @@ std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
     return "the split's scales and biases do not fit in LDS (split K further)";
   if (q.ksplit > 1 && ring_tiles(M, N, q.tile_n) > kMaxStrips)
     return "too many output tiles to split K";
+  if (q.ksplit > 1 && (size_t)q.ksplit * ring_tiles(M, N, q.tile_n) * 128 * q.tile_n * 4 >=
+                          (1ull << 32))
+    return "the partial sums would exceed 4 GiB";
   return "";
 }
 
@@ -852,8 +855,8 @@ std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
 // when N allows it, with 128 x 192 tiles (eight-wave workgroups) unsplit when they give at
 // least half a workgroup per CU (up projection 1536 x 8960: 188 workgroups, 30.6 us; 128 x 160
 // four-wave tiles 31.3 us; the best register-staged plan 42.4 us), else 128 x 96 tiles with K
-// split to about one workgroup per CU (down projection 8960 x 1536: four splits, 36.4 us;
-// 128 x 64 in five splits 36.9 us; register-staged 47.0 us); the register-staged kernel
+// split to about one workgroup per CU (down projection 8960 x 1536: four splits, 33.9 us;
+// 128 x 128 in five splits 35.0 us; register-staged 47.0 us); the register-staged kernel
 // otherwise: 128 x 128 tiles when they give about one workgroup per CU, else 64 x 64, K split
 // to about three workgroups per CU keeping 24 steps per split.
 GemmPlan planner_gemm(int M, int K, int N) {
@@ -939,7 +942,10 @@ size_t gemm_workspace(int M, int K, int N, int group_size) {
   for (int dtype : {MT_BF16, MT_F16}) {
     const GemmPlan g = plan_gemm(M, K, N, group_size, dtype);
     if (g.ksplit > 1) {
-      const size_t b = kCounterBytes + (size_t)g.ksplit * M * N * 4;
+      // kernel 0: [ksplit][M][N] fp32 partial sums; kernel 1: [ksplit][tile][128 x tile_n] in
+      // the accumulators' register layout
+      const size_t part = g.kernel == 0 ? (size_t)M * N : (size_t)g.tiles * 128 * g.tile_n;
+      const size_t b = kCounterBytes + (size_t)g.ksplit * part * 4;
       if (b > need) need = b;
     }
   }
