@@ -311,20 +311,29 @@ __global__ __launch_bounds__(64 * kBlockMaxWaves) void affine_block_kernel(const
     const int c = 16 * t + (l & 15), m0 = 16 * rt + 4 * (l >> 4);
     if (c >= width || m0 >= M) continue;
     f32x4 v[NPROJ];
+    if (p.ksplit == 1) {
 #pragma unroll
-    for (int pr = 0; pr < NPROJ; ++pr) {
-      if (p.ksplit == 1) {
+      for (int pr = 0; pr < NPROJ; ++pr) {
         const int slot = (t * NPROJ + pr) * RT + rt;
         v[pr] = red4[slot * 64 + l];
         for (int w = 1; w < waves; ++w) v[pr] += red4[(w * kSlots + slot) * 64 + l];
-      } else {
+      }
+    } else {
+      // the job's 4 NPROJ outputs over all splits, their loads in flight together
+      const float* src[4 * NPROJ];
+      float sum[4 * NPROJ];
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          v[pr][r] = m0 + r < M ? sum_partials(p.partial + (size_t)pr * plane +
-                                                    (size_t)(m0 + r) * N + col0 + c,
-                                                (size_t)NPROJ * plane, p.ksplit)
-                                : 0.0f;
-      }
+          src[pr * 4 + r] = m0 + r < M ? p.partial + (size_t)pr * plane +
+                                             (size_t)(m0 + r) * N + col0 + c
+                                       : nullptr;
+      sum_partials_multi<4 * NPROJ>(src, (size_t)NPROJ * plane, p.ksplit, sum);
+#pragma unroll
+      for (int pr = 0; pr < NPROJ; ++pr)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[pr][r] = sum[pr * 4 + r];
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

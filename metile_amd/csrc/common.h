@@ -355,6 +355,34 @@ __device__ __forceinline__ float sum_partials(const float* p, size_t stride, int
   return acc;
 }
 
+// NV such sums at once: out[v] = ((0 + q[v][0]) + q[v][1]) + ... over n splits of ptr[v] (split
+// stride `stride` floats; a null pointer sums to 0), every load of a batch of splits (16 loads)
+// requested before any is added, so a batch costs one memory round trip.
+template <int NV>
+__device__ __forceinline__ void sum_partials_multi(const float* const (&ptr)[NV], size_t stride,
+                                                   int n, float (&out)[NV]) {
+  constexpr int kBatch = NV >= 16 ? 1 : 16 / NV;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) out[v] = 0.0f;
+  for (int b = 0; b < n; b += kBatch) {
+    float q[kBatch][NV];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        q[u][v] = b + u < n && ptr[v] ? __hip_atomic_load(ptr[v] + (size_t)(b + u) * stride,
+                                                          __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0.0f;
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (b + u < n) {
+#pragma unroll
+        for (int v = 0; v < NV; ++v) out[v] += q[u][v];
+      }
+  }
+}
+
 // silu(g) * u with the hardware reciprocal (1 ulp in fp32, far below the 16-bit rounding of the
 // result) instead of an IEEE division sequence. Large negative g: exp(-g) = inf, rcp(inf) = 0.
 __device__ __forceinline__ float silu_mul(float g, float u) {
