@@ -229,19 +229,30 @@ typedef struct mt_qmv_plan {
   int order;
 } mt_qmv_plan;
 
-/* How the prefill GEMM runs: the kernel, its output tile (tile_m x tile_n) and the number of K
- * splits. MT_GEMM_STAGED (v_mfma_f32_32x32x16, operands staged through registers into LDS):
- * square tiles of 64 or 128, K split into equal lengths. MT_GEMM_RING (v_mfma_f32_16x16x32,
- * activations and codes through three-stage LDS rings filled by buffer_load...lds): tiles of
- * 128 x 64, 96, 160 or 192, N a multiple of 8, at most 8 splits of whole three-step lengths
- * (steps of 64 along K). The reference's matmul plans race tile shapes the same way
- * (MLXAffineMatmulConfig, metile/backends/mlx_affine.py:36-63). */
+/* How the prefill GEMM runs: the kernel, its output tile (tile_m x tile_n), the number of K
+ * splits and the tile order. MT_GEMM_STAGED (v_mfma_f32_32x32x16, operands staged through
+ * registers into LDS): square tiles of 64 or 128, K split into equal lengths, order 0.
+ * MT_GEMM_RING (v_mfma_f32_16x16x32, activations and codes through three-stage LDS rings filled
+ * by buffer_load...lds): tiles of 128 x 64, 96, 128, 160, 192 or 256, N a multiple of 8, at most
+ * 8 splits of whole three-step lengths (steps of 64 along K), and the order in which workgroups
+ * take (column tile, row block, split): MT_GEMM_ORDER_GRID (row-major, as launched), or each of
+ * the 8 XCDs (which take workgroups in turn) a contiguous run of that sequence with column tiles
+ * (MT_GEMM_ORDER_XCD_COLUMNS) or row blocks (MT_GEMM_ORDER_XCD_ROWS) varying fastest, so that
+ * the tiles sharing activations or codes share an L2. The reference's matmul plans race tile
+ * shapes and tile orders the same way (MLXAffineMatmulConfig, metile/backends/mlx_affine.py:36-63,
+ * _candidate_configs :155-166). */
 typedef enum mt_gemm_kernel { MT_GEMM_STAGED = 0, MT_GEMM_RING = 1 } mt_gemm_kernel;
+typedef enum mt_gemm_order {
+  MT_GEMM_ORDER_GRID = 0,
+  MT_GEMM_ORDER_XCD_COLUMNS = 1,
+  MT_GEMM_ORDER_XCD_ROWS = 2
+} mt_gemm_order;
 typedef struct mt_gemm_plan {
   int kernel;
   int tile_m;
   int tile_n;
   int ksplit;
+  int order;
 } mt_gemm_plan;
 
 /* By default every call plans itself from its shape. A tuner lists the plans a shape can take,

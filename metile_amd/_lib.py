@@ -41,7 +41,7 @@ class GemmPlan(ctypes.Structure):
     """``mt_gemm_plan``."""
 
     _fields_ = [("kernel", ctypes.c_int), ("tile_m", ctypes.c_int), ("tile_n", ctypes.c_int),
-                ("ksplit", ctypes.c_int)]
+                ("ksplit", ctypes.c_int), ("order", ctypes.c_int)]
 
 
 class DensePlan(ctypes.Structure):

@@ -22,6 +22,8 @@ struct GemmParams {
   int ksplit;
   int steps_per_split;
   int sb_words;        // ring kernel: dwords of scales (and of biases) staged per column
+  int order;           // ring kernel: 0 grid order; 1, 2: each XCD a contiguous run of tiles,
+                       // column tiles (1) or row blocks (2) fastest
 };
 
 // Register-staged kernel (affine_gemm.hip).

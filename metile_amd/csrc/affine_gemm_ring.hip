@@ -97,9 +97,28 @@ __global__ __launch_bounds__(128 * WN) void affine_gemm_ring_kernel(const GemmPa
   const int wm = wave / WN, wn = wave % WN;
   const int i16 = lane & 15, g = lane >> 4;
   const int M = p.M, K = p.K, N = p.N;
-  const int m0 = blockIdx.y * 128, n0 = blockIdx.x * BN;
+  // Workgroup -> (column tile bx, row block by, split bz). Order 0: as launched. Orders 1 and 2:
+  // workgroups go to the 8 XCDs in turn (XCD = linear index % 8), so workgroup L takes item
+  // k T/8 + min(k, T%8) + L/8 (k = L % 8) of the sequence of T tiles, in which column tiles (1)
+  // or row blocks (2) vary fastest: each XCD gets a contiguous run of it.
+  int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  if (p.order) {
+    const int gx = gridDim.x, gy = gridDim.y, total = gx * gy * gridDim.z;
+    const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int k = lin & 7;
+    const int item = k * (total >> 3) + min(k, total & 7) + (lin >> 3);
+    if (p.order == 1) {
+      bx = item % gx;
+      by = (item / gx) % gy;
+    } else {
+      by = item % gy;
+      bx = (item / gy) % gx;
+    }
+    bz = item / (gx * gy);
+  }
+  const int m0 = by * 128, n0 = bx * BN;
   const int steps = K >> 6;
-  const int s_beg = blockIdx.z * p.steps_per_split;
+  const int s_beg = bz * p.steps_per_split;
   const int s_end = min(steps, s_beg + p.steps_per_split);
   const int gshift = __builtin_ctz((unsigned)p.G);
   const int gpr = K >> gshift;
@@ -286,9 +305,9 @@ __global__ __launch_bounds__(128 * WN) void affine_gemm_ring_kernel(const GemmPa
     // contiguous, device-coherent); the last to arrive adds the other splits' parts to its own
     // in split order (so the sum does not depend on which arrived last) and stores the tile.
     // Parts are [split][tile][128 BN] fp32.
-    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    const int tile = by * gridDim.x + bx;
     const int tiles = gridDim.x * gridDim.y;
-    const int split = blockIdx.z, parts = p.ksplit;
+    const int split = bz, parts = p.ksplit;
     constexpr uint32_t kPartBytes = 128u * BN * 4u;
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc(p.partial, (uint32_t)parts * (uint32_t)tiles * kPartBytes);

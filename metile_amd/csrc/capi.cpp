@@ -761,6 +761,7 @@ struct GemmPlan {
   int ksplit;
   int steps_per_split;
   int sb_words;  // kernel 1: scale (and bias) dwords staged per column
+  int order;     // kernel 1: tile order (MT_GEMM_ORDER_*)
 };
 
 int gemm_tiles(int M, int N, int tile) {
@@ -824,6 +825,8 @@ GemmPlan make_staged(int M, int K, int N, int tile, int ksplit) {
 std::string gemm_plan_problem(int M, int K, int N, const mt_gemm_plan& q) {
   const int steps = K / 64;
   if (q.ksplit < 1 || q.ksplit > steps) return "ksplit must be in 1..K/64";
+  if (q.order < 0 || q.order > 2) return "order must be 0, 1 or 2";
+  if (q.kernel == 0 && q.order != 0) return "kernel 0 takes order 0";
   if (q.kernel == 0) {
     if (q.tile_m != q.tile_n || (q.tile_m != 64 && q.tile_m != 128))
       return "kernel 0 takes square tiles of 64 or 128";
@@ -868,7 +871,7 @@ GemmPlan planner_gemm(int M, int K, int N) {
       int ks = tile_n == 192 ? 1 : (256 + tiles / 2) / tiles;
       ks = ks < 1 ? 1 : ks > mt::kGemmMaxSplits ? mt::kGemmMaxSplits : ks;
       for (; ks <= mt::kGemmMaxSplits && ks <= steps; ++ks) {
-        const mt_gemm_plan q{1, 128, tile_n, ring_split(steps, ks).ksplit};
+        const mt_gemm_plan q{1, 128, tile_n, ring_split(steps, ks).ksplit, 0};
         if (gemm_plan_problem(M, K, N, q).empty()) return make_ring(M, K, N, tile_n, q.ksplit);
       }
     }
@@ -899,16 +902,20 @@ bool find_gemm_plan(const PlanKey& key, mt_gemm_plan* out) {
 GemmPlan plan_gemm(int M, int K, int N, int group_size, int dtype) {
   mt_gemm_plan q;
   if (find_gemm_plan(gemm_key(M, K, N, group_size, dtype), &q)) {
-    if (q.kernel == 1) return make_ring(M, K, N, q.tile_n, q.ksplit);
+    if (q.kernel == 1) {
+      GemmPlan g = make_ring(M, K, N, q.tile_n, q.ksplit);
+      g.order = q.order;
+      return g;
+    }
     return make_staged(M, K, N, q.tile_m == 128 ? 2 : 1, q.ksplit);
   }
   return planner_gemm(M, K, N);
 }
 
 mt_gemm_plan gemm_to_public(const GemmPlan& g) {
-  if (g.kernel == 1) return mt_gemm_plan{1, 128, g.tile_n, g.ksplit};
+  if (g.kernel == 1) return mt_gemm_plan{1, 128, g.tile_n, g.ksplit, g.order};
   const int t = g.tile == 2 ? 128 : 64;
-  return mt_gemm_plan{0, t, t, g.ksplit};
+  return mt_gemm_plan{0, t, t, g.ksplit, 0};
 }
 
 std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
@@ -920,7 +927,7 @@ std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
       const Plan p = split_plan(steps, ks);
       if (p.ksplit == last) continue;
       last = p.ksplit;
-      const mt_gemm_plan q{0, tile, tile, p.ksplit};
+      const mt_gemm_plan q{0, tile, tile, p.ksplit, 0};
       if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
     }
   }
@@ -930,8 +937,10 @@ std::vector<mt_gemm_plan> gemm_candidates(int M, int K, int N) {
       const Plan p = ring_split(steps, ks);
       if (p.ksplit == last) continue;
       last = p.ksplit;
-      const mt_gemm_plan q{1, 128, tile_n, p.ksplit};
-      if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
+      for (int order : {MT_GEMM_ORDER_GRID, MT_GEMM_ORDER_XCD_COLUMNS, MT_GEMM_ORDER_XCD_ROWS}) {
+        const mt_gemm_plan q{1, 128, tile_n, p.ksplit, order};
+        if (gemm_plan_problem(M, K, N, q).empty()) out.push_back(q);
+      }
     }
   }
   return out;
@@ -1301,6 +1310,7 @@ int mt_affine_gemm(const void* x, const uint32_t* w_q, const void* scales, const
   p.ksplit = g.ksplit;
   p.steps_per_split = g.steps_per_split;
   p.sb_words = g.sb_words;
+  p.order = g.kernel == 1 ? g.order : 0;
   const hipError_t e =
       g.kernel == 1 ? mt::launch_affine_gemm_ring(p, dtype, static_cast<hipStream_t>(stream))
                     : mt::launch_affine_gemm(p, dtype, static_cast<hipStream_t>(stream));

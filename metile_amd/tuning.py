@@ -198,20 +198,22 @@ _GEMM_KERNEL_CODES = {v: k for k, v in _GEMM_KERNELS.items()}
 @dataclass(frozen=True)
 class GemmPlan:
     """One prefill GEMM plan (``mt_gemm_plan``): the kernel ("staged": square tiles of 64 or
-    128; "ring": tiles of 128 x 64, 96, 160 or 192), its tile and the K splits."""
+    128; "ring": tiles of 128 x 64 .. 256), its tile, the K splits and the tile order (ring:
+    0 as launched, 1 / 2 each XCD a contiguous run of tiles, column tiles / row blocks fastest)."""
 
     kernel: str
     tile_m: int
     tile_n: int
     ksplit: int
+    order: int = 0
 
     def to_c(self) -> _lib.GemmPlan:
         return _lib.GemmPlan(_GEMM_KERNEL_CODES[self.kernel], self.tile_m, self.tile_n,
-                             self.ksplit)
+                             self.ksplit, self.order)
 
     @classmethod
     def from_c(cls, p) -> "GemmPlan":
-        return cls(_GEMM_KERNELS[p.kernel], p.tile_m, p.tile_n, p.ksplit)
+        return cls(_GEMM_KERNELS[p.kernel], p.tile_m, p.tile_n, p.ksplit, p.order)
 
     def workgroups(self, rows: int, n: int) -> int:
         return -(-rows // self.tile_m) * -(-n // self.tile_n) * self.ksplit

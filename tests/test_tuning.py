@@ -357,6 +357,12 @@ def test_gemm_plans(clean_plans):
     assert {(c.kernel, c.tile_m, c.tile_n) for c in cands} == {
         ("staged", 64, 64), ("staged", 128, 128), ("ring", 128, 64), ("ring", 128, 96),
         ("ring", 128, 128), ("ring", 128, 160), ("ring", 128, 192), ("ring", 128, 256)}
+    # every ring plan in the three tile orders, the register-staged ones in grid order only
+    ring = [c for c in cands if c.kernel == "ring"]
+    assert {c.order for c in ring} == {0, 1, 2} and len(ring) % 3 == 0
+    assert all(GemmPlan(c.kernel, c.tile_m, c.tile_n, c.ksplit, o) in cands
+               for c in ring for o in (0, 1, 2))
+    assert all(c.order == 0 for c in cands if c.kernel == "staged")
     # ring splits are whole three-step lengths: 140 steps split 4 ways run 36 + 36 + 36 + 32
     assert GemmPlan("ring", 128, 64, 4) in cands and GemmPlan("ring", 128, 64, 3) in cands
     assert all(c.ksplit <= 8 for c in cands if c.kernel == "ring")
@@ -374,7 +380,9 @@ def test_gemm_plans(clean_plans):
                      (GemmPlan("staged", 128, 64, 1), "kernel 0 takes square tiles"),
                      (GemmPlan("ring", 128, 224, 1), "kernel 1 takes tiles of 128 x"),
                      (GemmPlan("ring", 64, 64, 1), "kernel 1 takes tiles of 128 x"),
-                     (GemmPlan("ring", 128, 64, 9), "at most 8 K splits")):
+                     (GemmPlan("ring", 128, 64, 9), "at most 8 K splits"),
+                     (GemmPlan("ring", 128, 96, 4, 3), "order must be 0, 1 or 2"),
+                     (GemmPlan("staged", 128, 128, 1, 1), "kernel 0 takes order 0")):
         with pytest.raises(ValueError, match=why):
             tuning.install_gemm_plan(m, k, n, 64, torch.bfloat16, bad)
     # 24 steps in five splits: lengths of 6 (whole three-step iterations) give only four
