@@ -957,7 +957,8 @@ def dispatches(op: str) -> tuple:
             out.append({"rows": bucket, "input_features": k, "output_features": n,
                         "dtype": str(dtype), "group_size": group_size, "bits": 4,
                         "device": device, "kernel": plan.kernel, "tile_m": plan.tile_m,
-                        "tile_n": plan.tile_n, "ksplit": plan.ksplit, "source": source})
+                        "tile_n": plan.tile_n, "ksplit": plan.ksplit, "order": plan.order,
+                        "source": source})
             continue
         if mem[0] != "qmv" or mem[7] != (2 if op == "swiglu" else 1):
             continue

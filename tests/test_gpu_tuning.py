@@ -272,8 +272,8 @@ def test_tuned_executor_and_gemm(monkeypatch, tmp_path):
     (seen,) = mt.mlx_affine_matmul_dispatches()
     assert (seen["rows"], seen["input_features"], seen["output_features"], seen["source"]) == (
         256, 1024, 1536, "measured")
-    assert tuning.GemmPlan(seen["kernel"], seen["tile_m"], seen["tile_n"],
-                           seen["ksplit"]) == tuning.gemm_plan(
+    assert tuning.GemmPlan(seen["kernel"], seen["tile_m"], seen["tile_n"], seen["ksplit"],
+                           seen["order"]) == tuning.gemm_plan(
         200, 1024, 1536, 64, torch.bfloat16)
     print(f"[tuner gemm 200x1024x1536] planner {gemm[0]['planner']} {gemm[0]['planner_us']} us, "
           f"chosen {gemm[0]['plan']} {gemm[0]['chosen_us']} us", flush=True)
