@@ -351,7 +351,7 @@ def test_gemm_plans(clean_plans):
     # the planner takes the ring kernel at config 4: 128 x 96 tiles in four splits (36 steps)
     # for the down projection, 128 x 192 tiles unsplit for the up projection
     assert planner == GemmPlan("ring", 128, 96, 4)
-    assert tuning.gemm_plan(512, 1536, 8960, 64, torch.bfloat16) == GemmPlan("ring", 128, 192, 1)
+    assert tuning.gemm_plan(512, 1536, 8960, 64, torch.bfloat16) == GemmPlan("ring", 128, 192, 1, 2)
     cands = tuning.gemm_plan_candidates(m, k, n, 64)
     assert planner in cands
     assert {(c.kernel, c.tile_m, c.tile_n) for c in cands} == {
