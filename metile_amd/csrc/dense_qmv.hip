@@ -270,14 +270,27 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
   }
   __syncthreads();
   if (!last_flag) return;
-  for (int o = tid; o < M * 32; o += kThreads) {
-    const int i = o >> 5, c = o & 31;
-    const size_t oi = (size_t)i * N + strip * 32 + c;
-    float v[NPROJ];
+  // A thread's outputs over every split, their loads requested in batches (sum_partials_multi)
+  // rather than one round trip per output: one output at up to 8 rows (the instances without
+  // staged activations), else up to 32 MT rows x 32 columns over the workgroup's threads.
+  constexpr int kOuts = XLDS ? 32 * 32 * MT / kThreads : 1;
+  const float* src[kOuts * NPROJ];
+  float sum[kOuts * NPROJ];
 #pragma unroll
-    for (int pr = 0; pr < NPROJ; ++pr) {
-      v[pr] = sum_partials(partg + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
-    }
+  for (int u = 0; u < kOuts; ++u) {
+    const int o = tid + u * kThreads;
+    const size_t oi = (size_t)(o >> 5) * N + strip * 32 + (o & 31);
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+      src[u * NPROJ + pr] = o < M * 32 ? partg + (size_t)pr * plane + oi : nullptr;
+  }
+  sum_partials_multi<kOuts * NPROJ>(src, (size_t)NPROJ * plane, p.ksplit, sum);
+#pragma unroll
+  for (int u = 0; u < kOuts; ++u) {
+    const int o = tid + u * kThreads;
+    if (o >= M * 32) break;
+    const size_t oi = (size_t)(o >> 5) * N + strip * 32 + (o & 31);
+    const float* v = sum + u * NPROJ;
     if constexpr (NPROJ == 2) {
       yg[oi] = typed_swiglu<DT>(v[0], v[1]);
     } else {
