@@ -347,16 +347,28 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   __syncthreads();
   // No workgroup barrier follows: one tile may return while the other finishes its strip.
   if (!flag[tile]) return;
-  for (int o = ttid; o < outs; o += kTileThreads) {
-    const int i = o >> 5, c = o & 31;
-    if (c >= width) continue;
-    const size_t oi = (size_t)i * N + col0 + c;
+  // A thread's outputs (one, two at 32 rows) over every split, requested in batches.
+  constexpr int kOuts = (MROWS * 32 + kTileThreads - 1) / kTileThreads;
+  const float* src[kOuts * NPROJ];
+  float sum[kOuts * NPROJ];
+#pragma unroll
+  for (int u = 0; u < kOuts; ++u) {
+    const int o = ttid + u * kTileThreads;
+    const bool ok = o < outs && (o & 31) < width;
+    const size_t oi = (size_t)(o >> 5) * N + col0 + (o & 31);
+#pragma unroll
+    for (int pr = 0; pr < NPROJ; ++pr)
+      src[u * NPROJ + pr] = ok ? p.partial + (size_t)pr * plane + oi : nullptr;
+  }
+  sum_partials_multi<kOuts * NPROJ>(src, (size_t)NPROJ * plane, p.ksplit, sum);
+#pragma unroll
+  for (int u = 0; u < kOuts; ++u) {
+    const int o = ttid + u * kTileThreads;
+    if (o >= outs || (o & 31) >= width) continue;
     float v[NPROJ];
 #pragma unroll
-    for (int pr = 0; pr < NPROJ; ++pr) {
-      v[pr] = sum_partials(p.partial + (size_t)pr * plane + oi, (size_t)NPROJ * plane, p.ksplit);
-    }
-    finish(i, c, v);
+    for (int pr = 0; pr < NPROJ; ++pr) v[pr] = sum[u * NPROJ + pr];
+    finish(o >> 5, o & 31, v);
   }
   if (ttid == 0)
     __hip_atomic_store(&p.counters[strip], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
