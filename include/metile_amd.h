@@ -214,12 +214,16 @@ int mt_dense_residual_qmv(const void* x, const void* w, const void* residual, vo
  * groups of 64 or more) runs `strips` workgroups per K split, each a block of N / strips
  * columns (at most 64, also when N is counted in the 4-column (4-bit) or 2-column (8-bit)
  * units of the repacked layout) whose `tiles` waves (1 to 8) take consecutive runs of the
- * split's K steps over every column of the block. `order` is 0 for every kernel but the GEMV. */
+ * split's K steps over every column of the block. The 4x4x4-MFMA GEMV kernel (MT_QMV_GEMV4: up
+ * to 4 rows, 4-bit codes, groups of 32 or more, no K split) runs `strips` = N / 4, N / 8 or
+ * N / 16 workgroups of 1, 2 or 4 groups of 4 columns whose `tiles` waves (1 to 8) split K in
+ * rounds of 512, at most four rounds each. `order` is 0 for every kernel but the GEMV. */
 typedef enum mt_qmv_kernel {
   MT_QMV_STAGED = 1,
   MT_QMV_REGISTER = 2,
   MT_QMV_GEMV = 3,
-  MT_QMV_BLOCK = 4
+  MT_QMV_BLOCK = 4,
+  MT_QMV_GEMV4 = 5
 } mt_qmv_kernel;
 typedef struct mt_qmv_plan {
   int kernel;

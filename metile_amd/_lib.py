@@ -24,6 +24,7 @@ MT_QMV_STAGED = 1
 MT_QMV_REGISTER = 2
 MT_QMV_GEMV = 3
 MT_QMV_BLOCK = 4
+MT_QMV_GEMV4 = 5
 MT_GEMM_STAGED = 0
 MT_GEMM_RING = 1
 MT_LAYOUT_MLX = 0

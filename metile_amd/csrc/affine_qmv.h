@@ -187,6 +187,23 @@ hipError_t launch_affine_block(const QmvParams& p, int bits, int dtype, int npro
                                int tiles, hipStream_t stream);
 
 
+// ---- 4x4x4-MFMA GEMV kernel (M <= 4, 4-bit codes, groups of 32 or more) ----------------------
+// A workgroup owns `cg` groups of 4 columns (of each projection; cg 1, 2 or 4) and all of K
+// (grid N / (4 cg)); its `waves` waves take consecutive runs of 512-wide K rounds, at most four
+// rounds each, and a wave's loads of all its rounds stay in flight together (below the 64 loads
+// a wave can count).
+constexpr int kGemv4MaxWaves = 8;
+__host__ __device__ constexpr int gemv4_loads_per_round(int nproj, int cg) {
+  return 4 + 3 * nproj * cg;
+}
+__host__ __device__ constexpr bool affine_gemv4_fits(int K, int waves, int nproj, int cg) {
+  return waves >= 1 && waves <= kGemv4MaxWaves && (cg == 1 || cg == 2 || cg == 4) &&
+         waves <= (K + 511) / 512 && ((K + 511) / 512 + waves - 1) / waves <= 4 &&
+         ((K + 511) / 512 + waves - 1) / waves * gemv4_loads_per_round(nproj, cg) < 64;
+}
+hipError_t launch_affine_gemv4(const QmvParams& p, int dtype, int nproj, int waves, int cg,
+                               hipStream_t stream);
+
 hipError_t launch_affine_dequantize(const uint32_t* w, const uint16_t* s, const uint16_t* b,
                                     float* out, int N, int K, int G, int bits, int dtype,
                                     hipStream_t stream);

@@ -355,6 +355,19 @@ std::string qmv_plan_problem(int rows, int K, int N, int nproj, int group_size, 
       return "the GEMV kernel does not hold this many columns and rows in registers";
     return "";
   }
+  if (q.kernel == MT_QMV_GEMV4) {
+    if (rows > 4) return "more rows than the 4x4x4-MFMA GEMV kernel takes";
+    if (bits != 4) return "the 4x4x4-MFMA GEMV kernel takes 4-bit codes";
+    if (q.ksplit != 1) return "the 4x4x4-MFMA GEMV kernel does not split K";
+    if (q.order != 0) return "order is a GEMV plan field (0 for the other kernels)";
+    const int cg = q.strips >= 1 && N % q.strips == 0 ? N / q.strips / 4 : 0;
+    if (cg * 4 * q.strips != N || (cg != 1 && cg != 2 && cg != 4))
+      return "the 4x4x4-MFMA GEMV kernel runs N/4, N/8 or N/16 workgroups";
+    if (!mt::affine_gemv4_fits(K, q.tiles, nproj, cg))
+      return "4x4x4-MFMA GEMV tiles (waves) must be in 1..8, at most the 512-wide K rounds, "
+             "with at most four rounds each and their loads within 64";
+    return "";
+  }
   if (q.kernel == MT_QMV_BLOCK) {
     if (group_size < 64) return "the block kernel takes groups of 64 or more";
     if (rows > mt::kBlockMaxRows) return "more rows than the block kernel takes";
@@ -472,6 +485,13 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
         const mt_qmv_plan g{MT_QMV_GEMV, 1, N / per_wg, w, order};
         if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
       }
+  // 4x4x4-MFMA GEMV: 1, 2 or 4 groups of 4 columns per workgroup, every wave count that fits.
+  for (int cg : {1, 2, 4})
+    for (int w = 1; w <= mt::kGemv4MaxWaves; ++w) {
+      if (N % (4 * cg)) continue;
+      const mt_qmv_plan g{MT_QMV_GEMV4, 1, N / (4 * cg), w, 0};
+      if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
+    }
   // Column blocks: one or two workgroups per CU, or blocks of 16 or 32 columns; 4 or 8 waves;
   // K unsplit or in 4 splits.
   {
@@ -618,6 +638,8 @@ int run_qmv(const char* op, int nproj, const void* x, const uint32_t* const w[2]
       e = mt::launch_affine_block(
           p, bits, dtype, nproj, plan.tiles,
           mt::block_tiles((units + plan.strips - 1) / plan.strips * p.col_align), hs);
+    else if (plan.kernel == MT_QMV_GEMV4)
+      e = mt::launch_affine_gemv4(p, dtype, nproj, plan.tiles, N / plan.strips / 4, hs);
     else if (plan.kernel == MT_QMV_GEMV)
       e = mt::launch_affine_gemv(p, bits, dtype, nproj, plan.tiles,
                                  N / plan.strips / mt::affine_gemv_groups(K, bits, plan.tiles),

@@ -68,7 +68,7 @@ CACHE_FILE = "affine-plans-v2.jsonl"
 _LAYOUT_MLX, _LAYOUT_REPACKED = 0, 1
 _LAYOUT_NAMES = {_LAYOUT_MLX: "mlx", _LAYOUT_REPACKED: "repacked"}
 _KERNELS = {_lib.MT_QMV_STAGED: "staged", _lib.MT_QMV_REGISTER: "register",
-            _lib.MT_QMV_GEMV: "gemv", _lib.MT_QMV_BLOCK: "block"}
+            _lib.MT_QMV_GEMV: "gemv", _lib.MT_QMV_BLOCK: "block", _lib.MT_QMV_GEMV4: "gemv4"}
 _KERNEL_CODES = {v: k for k, v in _KERNELS.items()}
 
 
@@ -168,10 +168,10 @@ def row_bucket(rows: int) -> int:
 class QmvPlan:
     """One small-row dispatch plan (``mt_qmv_plan``)."""
 
-    kernel: str  # "staged", "register", "gemv" or "block"
+    kernel: str  # "staged", "register", "gemv", "block" or "gemv4" (4x4x4-MFMA GEMV)
     ksplit: int
     strips: int
-    tiles: int = 1  # staged: strips per workgroup; gemv and block: waves per workgroup
+    tiles: int = 1  # staged: strips per workgroup; gemv, block and gemv4: waves per workgroup
     order: int = 0  # gemv: 0 index order, 1 column groups dealt out XCD by XCD
 
     def to_c(self) -> _lib.QmvPlan:
@@ -184,7 +184,7 @@ class QmvPlan:
 
     @property
     def workgroups(self) -> int:
-        if self.kernel == "gemv":
+        if self.kernel in ("gemv", "gemv4"):
             return self.strips
         if self.kernel == "block":
             return self.strips * self.ksplit

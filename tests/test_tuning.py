@@ -228,9 +228,20 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
     # blocks of 16 or 32 columns, at most 64 wide in either code layout; 4 or 8 waves; K unsplit
     # or in 4 equal splits; groups of 64 or more
     align = 16 // bits
+    # the 4x4x4-MFMA GEMV: up to 4 rows of 4-bit codes, 1, 2 or 4 groups of 4 columns per
+    # workgroup, every wave count that gives each wave one to four 512-wide K rounds whose loads
+    # (4 + 3 nproj groups each) stay below 64
+    rounds = -(-k // 512)
+    assert sorted((c.strips, c.tiles) for c in cands if c.kernel == "gemv4") == (
+        sorted((n // (4 * cg), w) for cg in (1, 2, 4) for w in range(1, 9)
+               if w <= rounds and -(-rounds // w) <= 4
+               and -(-rounds // w) * (4 + 3 * nproj * cg) < 64 and n % (4 * cg) == 0)
+        if bucket <= 4 and bits == 4 else [])
     for c in cands:
-        assert c.kernel in ("staged", "register", "gemv", "block")
-        if c.kernel == "register":
+        assert c.kernel in ("staged", "register", "gemv", "block", "gemv4")
+        if c.kernel == "gemv4":
+            assert c.ksplit == 1 and c.strips in (n // 4, n // 8, n // 16) and c.order == 0
+        elif c.kernel == "register":
             assert g != 32 and c.strips == n // 32 and c.tiles == 1
         elif c.kernel == "gemv":
             assert c.ksplit == 1 and c.workgroups == c.strips
@@ -534,3 +545,20 @@ def test_dispatches_report_the_plan_of_the_dispatch_rows_not_the_bucket(clean_pl
     got = QmvPlan(d["kernel"], d["ksplit"], d["strips"], d["tiles"], d["order"])
     assert (d["rows"], d["source"]) == (4, "planner")
     assert got == tuning.qmv_plan(3, k, n, 64, 4, 2, bf)
+
+
+def test_gemv4_plans_are_checked(clean_plans):
+    import torch
+
+    for rows, k, n, bits, plan, why in (
+            (5, 1536, 256, 4, QmvPlan("gemv4", 1, 64, 1), "more rows"),
+            (1, 1536, 256, 8, QmvPlan("gemv4", 1, 64, 1), "4-bit codes"),
+            (1, 1536, 256, 4, QmvPlan("gemv4", 2, 64, 1), "does not split K"),
+            (1, 1536, 256, 4, QmvPlan("gemv4", 1, 8, 1), "N/4, N/8 or N/16 workgroups"),
+            (1, 1536, 256, 4, QmvPlan("gemv4", 1, 64, 4), "rounds"),  # 3 rounds, 4 waves
+            (1, 8960, 256, 4, QmvPlan("gemv4", 1, 64, 4), "rounds")):  # 18 rounds: 5 per wave
+        with pytest.raises(ValueError, match=why):
+            tuning.install_qmv_plan(rows, k, n, 64, bits, 1, torch.bfloat16, plan)
+    ok = QmvPlan("gemv4", 1, 64, 3)
+    tuning.install_qmv_plan(4, 1536, 256, 32, 4, 2, torch.bfloat16, ok)
+    assert tuning.qmv_plan(3, 1536, 256, 32, 4, 2, torch.bfloat16) == ok
