@@ -3,8 +3,8 @@
 // SwiGLU epilogues :124-132, :204-214; mlx_affine_qmv, mlx_affine_residual_qmv,
 // mlx_affine_swiglu, metile/backends/mlx_quantized.py:691-751,1538-1720).
 //
-// A workgroup owns 4 output columns (of each projection) and all of K; its waves split K into
-// rounds of 512. In a round, the 16 blocks of the 4x4x4 MFMA take 16 segments of 32 K (block b:
+// A workgroup owns 4, 8 or 16 output columns (CG groups of 4, of each projection) and all of K;
+// its waves split K into rounds of 512. In a round, the 16 blocks of the 4x4x4 MFMA take 16 segments of 32 K (block b:
 // K0 + 32 b): lane l = 4 b + q supplies activation row q (A) and code column q (B), four K of its
 // segment per MFMA, eight MFMAs per segment, so one 16-byte code load per lane and column group
 // feeds a whole round and every code is multiplied once by all four rows. Codes are unpacked to
