@@ -264,6 +264,22 @@ def kernel_label(k, n, nproj):
     return f"affine_qmv_kernel<{BITS}, 0, ..., {nproj}, ...> ({plan.ksplit} K splits)"
 
 
+def kernel_label_rows(m, k, n, nproj):
+    """The kernel instance (4x4x4 GEMV, M=1 instances) or else the plan a dispatch of this shape
+    at ``m`` rows runs under the plan installed now."""
+    from metile_amd import tuning
+
+    plan = tuning.qmv_plan(m, k, n, GROUP, BITS, nproj, torch.bfloat16)
+    if plan.kernel == "gemv4":
+        rows = 1 if m <= 1 else 2 if m <= 2 else 4
+        rpw = -(-(-(-k // 512)) // plan.tiles)
+        return (f"affine_gemv4_kernel<0, {rows}, {nproj}, {n // plan.strips // 4}, {rpw}> "
+                f"({plan.strips} workgroups of {plan.tiles} waves)")
+    if m == 1:
+        return kernel_label(k, n, nproj)
+    return str(plan)
+
+
 def rate(nbytes, us):
     """GB/s of ``nbytes`` moved in ``us`` microseconds."""
     return round(nbytes / us / 1e3, 1)
@@ -628,6 +644,31 @@ def traffic_probe(mt, gen, device, args):
           flush=True)
 
 
+def rows_probe(mt, gen, device, args):
+    """Eager launches for the instruction-counter runs of the headline MLP at several rows: for
+    each row count of ``--rows``, three passes of the SwiGLU and then the down projection over
+    the 28-layer stack, in the layouts and plans of a tuned run (run with its decision cache and
+    METILE_AMD_DISABLE_TUNING=1). Prints each row count's layouts and dispatch order."""
+    native, packed = make_stack(mt, gen, device)
+    phases = []
+    for m in [int(r) for r in args.rows.split(",")]:
+        layers, layouts = stack_layers(args, gen, device, native, packed, m)
+        x = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+        res = torch.randn(m, HIDDEN, generator=gen, device=device).to(torch.bfloat16)
+        h = torch.randn(m, INTER, generator=gen, device=device).to(torch.bfloat16)
+        for _ in range(3):
+            for g, u, _d in layers:
+                mt.affine_swiglu(x, *g, *u, group_size=GROUP, bits=BITS)
+        for _ in range(3):
+            for _g, _u, d in layers:
+                mt.affine_qmv(h, *d, group_size=GROUP, bits=BITS, residual=res)
+        torch.cuda.synchronize()
+        phases.append({"rows": m, "layouts": layouts,
+                       "swiglu": kernel_label_rows(m, HIDDEN, INTER, 2),
+                       "down": kernel_label_rows(m, INTER, HIDDEN, 1)})
+    print(json.dumps({"rows_probe": "done", "phases": phases}), flush=True)
+
+
 def prefill_probe(mt, gen, device, args):
     """Eager launches for the prefill GEMM counter runs: three of each config-4 projection, with
     the plan of a tuned run when its decision cache is given (METILE_AMD_DISABLE_TUNING=1)."""
@@ -776,6 +817,9 @@ def main():
                     help="only the eager launches profiled by the HBM-traffic counter runs")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only eager config-4 GEMM launches, for instruction-counter runs")
+    ap.add_argument("--rows-probe", action="store_true",
+                    help="only eager headline SwiGLU/down launches at each --rows row count, for "
+                         "instruction-counter runs")
     ap.add_argument("--no-tune", action="store_true",
                     help="run every shape on the planner's plan (no plan tuning)")
     ap.add_argument("--details", default=os.path.join("gpurun_out", "bench_details.json"),
@@ -803,6 +847,9 @@ def main():
         return
     if args.prefill_probe:
         prefill_probe(mt, gen, device, args)
+        return
+    if args.rows_probe:
+        rows_probe(mt, gen, device, args)
         return
 
     with torch.cuda.stream(stream):

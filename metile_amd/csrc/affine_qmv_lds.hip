@@ -20,8 +20,13 @@
 namespace mt {
 namespace {
 
-// Code stages each wave requests before the workgroup parks its scales and activations.
-constexpr int kQmvEarlyStages = 2;
+// Code stages each wave requests before the workgroup parks its scales and activations: one for
+// the three-stage 4-bit ring of a one-split short K (its waves have at most three steps, and
+// every code request ahead of the activations delays the staging all steps wait for: config-1
+// SwiGLU at M=16 8.55 -> 8.31 us, one projection 6.26 -> 6.03 us against two), else two (the
+// six-stage ring of a long K split: the down projection at M=16 8.14 us, 8.37 with one).
+template <int BITS, int STAGES, bool HALF>
+constexpr int qmv_early_stages() { return BITS == 4 && STAGES == 3 && !HALF ? 1 : 2; }
 
 // One workgroup's share: TILES consecutive output strips (strip s = columns [s N / strips,
 // (s + 1) N / strips), at most 32), strips [group TILES, group TILES + TILES), over K split
@@ -382,9 +387,8 @@ void affine_qmv_lds_kernel(const QmvParams args) {
   const QmvParams p = preload_args(args);  // all arguments in one batch of scalar loads
   extern __shared__ __align__(16) unsigned char dyn_plain[];
   __shared__ int flag[TILES];
-  lds_task<BITS, DT, MROWS, NPROJ, STAGES, kQmvEarlyStages, HALF, TILES>(p, blockIdx.x,
-                                                                         blockIdx.y, dyn_plain,
-                                                                         flag);
+  lds_task<BITS, DT, MROWS, NPROJ, STAGES, qmv_early_stages<BITS, STAGES, HALF>(), HALF, TILES>(
+      p, blockIdx.x, blockIdx.y, dyn_plain, flag);
 }
 
 // Raises a kernel's dynamic LDS limit (64 KiB by default) to what a workgroup of `tiles`
