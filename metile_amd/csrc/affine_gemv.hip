@@ -67,7 +67,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
   constexpr int kCodes = 128 / BITS;       // codes per chunk
   constexpr int kXLoads = kCodes / 8;      // 16-byte activation loads per chunk and row
   constexpr int kOut = NPROJ * COLS * ROWS;
-  constexpr float kOff = CodeOffset<BITS, DT>::value;
+  constexpr float kOff = SumOffset<BITS, DT>::value;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -165,11 +165,11 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 #pragma unroll
         for (int v = 0; v < kXLoads; ++v) {
           if constexpr (BITS == 4) {
-            cw[v] = unpack_u4_paired(S.q[pr][j][v], pc);
+            cw[v] = codes_for_sum<DT>(unpack_u4_paired(S.q[pr][j][v], pc));
           } else {
             const u32x2 lo = unpack_u8<DT>(S.q[pr][j][2 * v]);
             const u32x2 hi = unpack_u8<DT>(S.q[pr][j][2 * v + 1]);
-            cw[v] = (u32x4){lo.x, lo.y, hi.x, hi.y};
+            cw[v] = codes_for_sum<DT>((u32x4){lo.x, lo.y, hi.x, hi.y});
           }
         }
         const float sf = act_to_f32<DT>(S.s[pr][j]);

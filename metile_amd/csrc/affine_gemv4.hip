@@ -36,13 +36,6 @@ __device__ __forceinline__ f32x4 mfma4(u32x2 a, u32x2 b, f32x4 c) {
                                               __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
 }
 
-// Two f16 codes 1024 + q -> q, exactly (one packed 16-bit subtraction). The word arrives as a
-// scalar: a bit cast applied to an element of a vector value read the vector's first word.
-__device__ __forceinline__ uint32_t f16_minus_offset(uint32_t w) {
-  const f16x2 off = (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
-  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w) - off);
-}
-
 constexpr int kRoundK = 512;  // K per round: 16 blocks x 32
 constexpr int kDppRowRor4 = 0x124;  // row_ror:4 (lane i reads lane i + 4 of its row)
 constexpr int kDppRowRor8x = 0x128;  // row_ror:8
@@ -136,10 +129,7 @@ __global__ __launch_bounds__(64 * kGemv4MaxWaves) void affine_gemv4_kernel(const
     for (int u = 0; u < 4; ++u)
 #pragma unroll
       for (int c = 0; c < kSlots; ++c) {
-        u32x4 cw = unpack_u4_paired(S.w[c][u], pc);
-        if constexpr (DT == kF16)
-          cw = (u32x4){f16_minus_offset(cw.x), f16_minus_offset(cw.y), f16_minus_offset(cw.z),
-                       f16_minus_offset(cw.w)};
+        const u32x4 cw = codes_for_sum<DT>(unpack_u4_paired(S.w[c][u], pc));
         t[c] = mfma4<DT>((u32x2){a[u].x, a[u].y}, (u32x2){cw.x, cw.y}, t[c]);
         t[c] = mfma4<DT>((u32x2){a[u].z, a[u].w}, (u32x2){cw.z, cw.w}, t[c]);
       }

@@ -54,7 +54,7 @@ template <int BITS, int DT, int MROWS, int NPROJ, int WAVES, int STAGES>
 __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams args) {
   const QmvParams p = preload_args(args);  // all arguments in one batch of scalar loads
   constexpr int kThreads = WAVES * 64;
-  constexpr float kOff = CodeOffset<BITS, DT>::value;
+  constexpr float kOff = SumOffset<BITS, DT>::value;
   constexpr int kRegs = MROWS / 2;  // accumulator registers holding rows < MROWS
   constexpr int kArrays = 2 * NPROJ;  // scales and biases of each projection
 
@@ -166,9 +166,10 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
         const int gl = (st >> gshift) - g_beg + sb_shift;
 #pragma unroll
         for (int pr = 0; pr < NPROJ; ++pr) {
-          f32x16 t = mfma32<DT>(S.x[0], code_frag<BITS, DT>(S.w[pr], 0), zero16);
+          f32x16 t = mfma32<DT>(S.x[0], codes_for_sum<DT>(code_frag<BITS, DT>(S.w[pr], 0)), zero16);
 #pragma unroll
-          for (int e = 1; e < 4; ++e) t = mfma32<DT>(S.x[e], code_frag<BITS, DT>(S.w[pr], e), t);
+          for (int e = 1; e < 4; ++e)
+            t = mfma32<DT>(S.x[e], codes_for_sum<DT>(code_frag<BITS, DT>(S.w[pr], e)), t);
           const float sf = act_to_f32<DT>(sb16[((2 * pr) * 32 + j) * 2 * kSbRowWords + gl]);
           const float bf = act_to_f32<DT>(sb16[((2 * pr + 1) * 32 + j) * 2 * kSbRowWords + gl]);
           const float bp = __builtin_fmaf(-kOff, sf, bf);

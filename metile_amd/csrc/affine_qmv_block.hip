@@ -46,9 +46,10 @@ __global__ __launch_bounds__(64 * kBlockMaxWaves) void affine_block_kernel(const
   const QmvParams p = preload_args(args);
   constexpr int D = block_ring(BITS, NPROJ, RT, TPB);
   constexpr int kCols = 16 * TPB;
-  constexpr float kOff = CodeOffset<BITS, DT>::value;
-  // B operand of the row-sum MFMA: -offset (two 16-bit floats per word), or 1 when codes are
-  // exact integers with no offset (8-bit bf16); the bias then multiplies by kXScale of it.
+  constexpr float kOff = SumOffset<BITS, DT>::value;
+  // B operand of the row-sum MFMA: -offset (two 16-bit floats per word), or 1 when the codes
+  // multiplied are the integers themselves (8-bit bf16, f16); the bias then multiplies by
+  // kXScale of it.
   constexpr uint32_t kXB = kOff == 0.0f ? (DT == kBF16 ? 0x3F803F80u : 0x3C003C00u)
                                         : (DT == kBF16 ? (BITS == 4 ? 0xC300C300u : 0u)
                                                        : 0xE400E400u);
@@ -213,14 +214,14 @@ __global__ __launch_bounds__(64 * kBlockMaxWaves) void affine_block_kernel(const
       for (int pr = 0; pr < NPROJ; ++pr) {
         u32x4 b0, b1;
         if constexpr (BITS == 4) {
-          b0 = unpack_u4_paired(S.c[t][pr].x, pc);
-          b1 = unpack_u4_paired(S.c[t][pr].y, pc);
+          b0 = codes_for_sum<DT>(unpack_u4_paired(S.c[t][pr].x, pc));
+          b1 = codes_for_sum<DT>(unpack_u4_paired(S.c[t][pr].y, pc));
         } else {
           const CodeT w = S.c[t][pr];
           const u32x2 l0 = unpack_u8<DT>(w.x), l1 = unpack_u8<DT>(w.y);
           const u32x2 h0 = unpack_u8<DT>(w.z), h1 = unpack_u8<DT>(w.w);
-          b0 = (u32x4){l0.x, l0.y, l1.x, l1.y};
-          b1 = (u32x4){h0.x, h0.y, h1.x, h1.y};
+          b0 = codes_for_sum<DT>((u32x4){l0.x, l0.y, l1.x, l1.y});
+          b1 = codes_for_sum<DT>((u32x4){h0.x, h0.y, h1.x, h1.y});
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {

@@ -42,7 +42,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
   constexpr int WAVES = kQmvLdsWaves;  // per tile
   constexpr int kTileThreads = WAVES * 64;
   constexpr int kThreads = kTileThreads * TILES;
-  constexpr float kOff = CodeOffset<BITS, DT>::value;
+  constexpr float kOff = SumOffset<BITS, DT>::value;
   constexpr int kRegs = MROWS / 2;
   constexpr int kArrays = 2 * NPROJ;
   constexpr int kXIters = qmv_lds_chunk_iters(MROWS, TILES);
@@ -258,8 +258,8 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
           u32x4 b[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if constexpr (BITS == 4) b[e] = unpack_u4_paired(S[pr][0][e], pc);
-            else b[e] = code_frag<BITS, DT>(S[pr], e);
+            if constexpr (BITS == 4) b[e] = codes_for_sum<DT>(unpack_u4_paired(S[pr][0][e], pc));
+            else b[e] = codes_for_sum<DT>(code_frag<BITS, DT>(S[pr], e));
           }
 #pragma unroll
           for (int g = 0; g < kHalves; ++g) {

@@ -244,6 +244,32 @@ __device__ __forceinline__ u32x4 code_frag(const u32x4 (&w)[BITS / 4], int e) {
   }
 }
 
+// f16 codes without their offset: 1024 + q minus 1024 is exact in f16 (one packed subtraction
+// per word of two codes). The small-row kernels multiply q itself, so that their fp32 sums do not
+// carry 1024 times the activation sums (seven bits more rounding than bf16's 128 + q);
+// SumOffset is the offset the codes they multiply still hold. The word arrives as a scalar: a
+// bit cast applied to an element of a vector value read the vector's first word.
+__device__ __forceinline__ uint32_t f16_minus_offset(uint32_t w) {
+  const f16x2 off = (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, w) - off);
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 codes_for_sum(u32x4 v) {
+  if constexpr (DT == kF16) {
+    const uint32_t x = v.x, y = v.y, z = v.z, w = v.w;
+    return (u32x4){f16_minus_offset(x), f16_minus_offset(y), f16_minus_offset(z),
+                   f16_minus_offset(w)};
+  } else {
+    return v;
+  }
+}
+
+template <int BITS, int DT>
+struct SumOffset {
+  static constexpr float value = DT == kF16 ? 0.0f : CodeOffset<BITS, DT>::value;
+};
+
 // The two 16-bit floats of a packed pair, widened to fp32 (element 0 is the low half).
 template <int DT>
 __device__ __forceinline__ float lo16(uint32_t w) {

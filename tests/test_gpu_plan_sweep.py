@@ -1,0 +1,104 @@
+"""Every listed plan at seeded random small-row shapes, on the GPU through the C ABI.
+
+The plan-listing functions (``mt_affine_qmv_plan_candidates``) and the plan checker decide which
+plans the tuner may install for a shape; the bench-shape sweep in ``test_gpu_tuning.py`` covers
+the shapes ``bench.py`` times. This sweep draws other shapes under the API's constraints (K a
+multiple of 64 and of the group, N a multiple of 32, groups of 32/64/128, 4 and 8 bits, one or
+two projections, with and without the residual, bf16 and f16, 1 to 32 rows) plus the edge
+shapes (one K step, one 32-column strip, K of one group of 128), and holds every listed plan to
+the contract: within ``tolerance_error`` 2e-3 of the oracle, >= 98% (bf16) / 90% (f16) of the
+outputs equal to the correctly rounded value, and the MLX-layout and repacked codes
+bit-identical.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import metile_amd as mt
+from metile_amd import tuning
+from oracle import affine as O
+from tests.helpers import act_to_torch, affine_to_torch, torch_to_act
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _shapes():
+    rng = np.random.RandomState(2026)
+    out = []
+    for _ in range(12):
+        g = int(rng.choice([32, 64, 128]))
+        k = int(rng.randint(1, 40)) * 128 if g == 128 else int(rng.randint(1, 48)) * 64
+        n = int(rng.randint(1, 48)) * 32
+        rows = int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16, 24, 32]))
+        rows = min(rows, 16) if g == 32 else rows  # one dispatch holds 16 rows at groups of 32
+        bits = int(rng.choice([4, 8]))
+        nproj = int(rng.choice([1, 2]))
+        residual = nproj == 1 and bool(rng.randint(2))
+        dtype = "f16" if rng.randint(4) == 0 else "bf16"
+        out.append((rows, k, n, g, bits, nproj, residual, dtype))
+    # edge shapes: one K step, one strip, one group of 128, most rows
+    out += [(1, 64, 32, 64, 4, 1, True, "bf16"), (16, 64, 32, 32, 8, 2, False, "bf16"),
+            (7, 128, 96, 128, 4, 2, False, "f16"), (32, 640, 32, 64, 4, 1, True, "bf16")]
+    return out
+
+
+SHAPES = _shapes()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    torch.cuda.set_device(0)
+
+
+@pytest.fixture(autouse=True)
+def _clean_plans():
+    tuning.clear_plans()
+    yield
+    tuning.clear_plans()
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_every_listed_plan_at_random_shapes(shape):
+    rows, k, n, g, bits, nproj, residual, dtype = shape
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    weights = [O.make_affine_weight(n, k, bits, g, 31, 10 + 2 * p, dtype) for p in range(nproj)]
+    x = O.make_activations(rows, k, 31, dtype=dtype)
+    res = O.make_activations(rows, n, 31, tensor_id=3, dtype=dtype) if residual else None
+    if nproj == 2:
+        ref = O.affine_swiglu(x, weights[0], weights[1], g, bits, dtype=dtype)
+    else:
+        ref = O.affine_qmv(x, *weights[0], g, bits, residual=res, dtype=dtype)
+    xt = act_to_torch(x, dtype)
+    rt = None if res is None else act_to_torch(res, dtype)
+    mlx = [affine_to_torch(w, dtype) for w in weights]
+    packed = [(mt.affine_repack(w, bits=bits), s, b) for (w, s, b) in mlx]
+
+    def run(ts):
+        if nproj == 2:
+            return mt.affine_swiglu(xt, *ts[0], *ts[1], group_size=g, bits=bits)
+        return mt.affine_qmv(xt, *ts[0], group_size=g, bits=bits, residual=rt)
+
+    min_exact = 0.98 if dtype == "bf16" else 0.90
+    want = O.to_f32(O.from_f32(ref.astype(np.float32), dtype), dtype)
+    cands = tuning.qmv_plan_candidates(rows, k, n, g, bits, nproj)
+    assert cands
+    kinds = set()
+    for plan in cands:
+        print(f"[{shape}] plan {plan}", flush=True)
+        tuning.install_qmv_plan(rows, k, n, g, bits, nproj, tdt, plan)
+        a, b = run(mlx), run(packed)
+        torch.cuda.synchronize()
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), plan
+        y = torch_to_act(a, dtype)
+        err = O.tolerance_error(y, ref, dtype)
+        exact = np.mean(O.to_f32(y, dtype) == want)
+        assert err <= TOL and exact >= min_exact, (plan, err, exact)
+        kinds.add(plan.kernel)
+    print(f"[{shape}] {len(cands)} plans over {sorted(kinds)}", flush=True)
