@@ -2,7 +2,7 @@
 
 The plan-listing functions (``mt_affine_qmv_plan_candidates``) and the plan checker decide which
 plans the tuner may install for a shape; the bench-shape sweep in ``test_gpu_tuning.py`` covers
-the shapes ``bench.py`` times. This sweep draws other shapes under the API's constraints (K a
+the shapes ``bench.py`` times. This sweep draws 40 other shapes under the API's constraints (K a
 multiple of 64 and of the group, N a multiple of 32, groups of 32/64/128, 4 and 8 bits, one or
 two projections, with and without the residual, bf16 and f16, 1 to 32 rows) plus the edge
 shapes (one K step, one 32-column strip, K of one group of 128), and holds every listed plan to
@@ -30,7 +30,7 @@ TOL = 2e-3
 def _shapes():
     rng = np.random.RandomState(2026)
     out = []
-    for _ in range(12):
+    for _ in range(40):
         g = int(rng.choice([32, 64, 128]))
         k = int(rng.randint(1, 40)) * 128 if g == 128 else int(rng.randint(1, 48)) * 64
         n = int(rng.randint(1, 48)) * 32
