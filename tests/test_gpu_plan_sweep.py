@@ -8,7 +8,8 @@ two projections, with and without the residual, bf16 and f16, 1 to 32 rows) plus
 shapes (one K step, one 32-column strip, K of one group of 128), and holds every listed plan to
 the contract: within ``tolerance_error`` 2e-3 of the oracle, >= 98% (bf16) / 90% (f16) of the
 outputs equal to the correctly rounded value, and the MLX-layout and repacked codes
-bit-identical.
+bit-identical. The whole MLP entry is checked likewise at 16 random shapes, each weight in a
+code layout drawn for it (85% exact end to end: the hidden activation's rounding can flip).
 """
 
 from __future__ import annotations
@@ -102,3 +103,47 @@ def test_every_listed_plan_at_random_shapes(shape):
         assert err <= TOL and exact >= min_exact, (plan, err, exact)
         kinds.add(plan.kernel)
     print(f"[{shape}] {len(cands)} plans over {sorted(kinds)}", flush=True)
+
+
+def _mlp_shapes():
+    rng = np.random.RandomState(99)
+    out = []
+    for _ in range(16):
+        g = int(rng.choice([32, 64, 128]))
+        h = int(rng.randint(1, 17)) * 128
+        i = int(rng.randint(1, 25)) * 128
+        rows = int(rng.choice([1, 2, 3, 4, 6, 8, 13, 16, 32]))
+        rows = min(rows, 16) if g == 32 else rows
+        bits = int(rng.choice([4, 8]))
+        dtype = "f16" if rng.randint(4) == 0 else "bf16"
+        layouts = (bool(rng.randint(2)), bool(rng.randint(2)))  # gate/up, down repacked
+        out.append((rows, h, i, g, bits, dtype, layouts, bool(rng.randint(2))))
+    return out
+
+
+@pytest.mark.parametrize("shape", _mlp_shapes(), ids=lambda s: "x".join(map(str, s)))
+def test_mlp_at_random_shapes(shape):
+    # the whole MLP entry (one C-ABI call, hidden activation in the workspace) under the
+    # planner's plans, each weight in the code layout drawn for it
+    rows, h, i, g, bits, dtype, (up_rep, down_rep), residual = shape
+    gate = O.make_affine_weight(i, h, bits, g, 37, 10, dtype)
+    up = O.make_affine_weight(i, h, bits, g, 37, 12, dtype)
+    down = O.make_affine_weight(h, i, bits, g, 37, 14, dtype)
+    x = O.make_activations(rows, h, 37, dtype=dtype)
+    res = O.make_activations(rows, h, 37, tensor_id=3, dtype=dtype) if residual else None
+    ref, _ = O.affine_mlp(x, gate, up, down, g, bits, residual=res, dtype=dtype)
+
+    def weights(w, rep):
+        wt, s, b = affine_to_torch(w, dtype)
+        return (mt.affine_repack(wt, bits=bits) if rep else wt), s, b
+
+    y = mt.affine_mlp(act_to_torch(x, dtype), weights(gate, up_rep), weights(up, up_rep),
+                      weights(down, down_rep), group_size=g, bits=bits,
+                      residual=None if res is None else act_to_torch(res, dtype))
+    got = torch_to_act(y, dtype)
+    err = O.tolerance_error(got, ref, dtype)
+    want = O.to_f32(O.from_f32(ref.astype(np.float32), dtype), dtype)
+    exact = np.mean(O.to_f32(got, dtype) == want)
+    print(f"[mlp {shape}] tolerance_error={err:.2e} exact={exact:.4f}", flush=True)
+    # end to end the hidden activation's rounding can flip, so 85% (both dtypes)
+    assert err <= TOL and exact >= 0.85, (err, exact)
