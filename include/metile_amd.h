@@ -19,6 +19,9 @@
  *                         word k/(32/bits) at bit (k % (32/bits))*bits (low bits first)
  *   scales, biases        16-bit floats [N, K/group_size], same dtype as x
  *   dense weights         16-bit floats [N, K]
+ * Kernels read x, w_q, dense weights and workspaces with 16-byte loads: these pointers must be
+ * 16-byte aligned (allocations are; a row slice of a conforming tensor stays aligned, since
+ * K % 64 == 0 and N % 32 == 0). Scales and biases need 4-byte alignment. Nothing checks this.
  */
 #ifndef METILE_AMD_H
 #define METILE_AMD_H
