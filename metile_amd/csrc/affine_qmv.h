@@ -58,7 +58,7 @@ hipError_t launch_affine_qmv(const QmvParams& p, int bits, int dtype, int nproj,
 // LDS row (in 32-bit words) of one column's scales or biases over a split's groups.
 constexpr int kSbRowWords = kMaxGroupsPerSplit / 2 + 2;
 
-// ---- activation-staged small-row kernels (M <= 16) --------------------------------------
+// ---- activation-staged small-row kernels (M <= 32; 16 for groups of 32) -----------------
 // Eight waves per strip ("tile"), one or two tiles per workgroup; the workgroup's activation
 // rows for its K range live in LDS, shared by its tiles.
 constexpr int kQmvLdsWaves = 8;
@@ -112,8 +112,8 @@ hipError_t launch_affine_qmv_lds(const QmvParams& p, int bits, int dtype, int np
                                  hipStream_t stream);
 
 // ---- GEMV kernel (M <= 4, no K split) ----------------------------------------------------
-// Workgroups of `waves` waves (1 to kGemvMaxWaves) each own `cols` output columns (2 or 4;
-// grid N / cols) and all of K; reads x, w, s, b, residual, y, M, K, N, G and the code layout
+// Workgroups of `waves` waves (1 to kGemvMaxWaves) each own `cols` output columns (2, 4 or 8)
+// per column group and all of K; reads x, w, s, b, residual, y, M, K, N, G and the code layout
 // of p.
 constexpr int kGemvMaxRows = 4;
 constexpr int kGemvMaxWaves = 8;

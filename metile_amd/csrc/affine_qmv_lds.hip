@@ -1,4 +1,4 @@
-// Activation-staged small-row affine projections (M <= 16) for gfx950.
+// Activation-staged small-row affine projections (M <= 32) for gfx950.
 //
 // Same contract as affine_qmv.hip: y[m, n] = sum_k x[m, k] * (q[n, k] * s[n, k/G] + b[n, k/G])
 // (reference semantics kernels/affine_qmv.py:4-54; residual and SwiGLU epilogues
