@@ -120,7 +120,7 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
 #pragma unroll
       for (int j = 0; j < COLS; ++j) {
         const uint32_t col = (uint32_t)(col0 + j);
-        S.q[pr][j] = load16(rw[pr], oob_unless(ok, col * p.col_stride + wo));
+        S.q[pr][j] = load16_nt(rw[pr], oob_unless(ok, col * p.col_stride + wo));
         const uint32_t go =
             oob_unless(ok, (col * (uint32_t)groups_per_row + (uint32_t)(k0 >> gshift)) * 2u);
         S.s[pr][j] = load2(rs[pr], go);

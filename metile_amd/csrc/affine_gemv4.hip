@@ -95,7 +95,7 @@ __global__ __launch_bounds__(64 * kGemv4MaxWaves) void affine_gemv4_kernel(const
       const uint32_t go = (col * (uint32_t)gpr + (uint32_t)(k >> gshift)) * 2u;
 #pragma unroll
       for (int pr = 0; pr < NPROJ; ++pr) {
-        R[r].w[pr * CG + cg] = load16(rw[pr], oob_unless(ok, col * p.col_stride + wk));
+        R[r].w[pr * CG + cg] = load16_nt(rw[pr], oob_unless(ok, col * p.col_stride + wk));
         R[r].s[pr * CG + cg] = load2(rs[pr], oob_unless(ok, go));
         R[r].bias[pr * CG + cg] = load2(rb[pr], oob_unless(ok, go));
       }

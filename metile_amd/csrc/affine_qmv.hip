@@ -124,7 +124,7 @@ __global__ __launch_bounds__(WAVES * 64) void affine_qmv_kernel(const QmvParams 
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
       for (int v = 0; v < BITS / 4; ++v)
-        S.w[pr][v] = load16(rw[pr], ok ? woff + 16u * v : kOOB);
+        S.w[pr][v] = load16_nt(rw[pr], ok ? woff + 16u * v : kOOB);
     const bool xok = ok && x_row != kOOB;
     const uint32_t xoff = x_row + (uint32_t)st * 128u;
 #pragma unroll

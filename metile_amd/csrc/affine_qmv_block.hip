@@ -151,9 +151,9 @@ __global__ __launch_bounds__(64 * kBlockMaxWaves) void affine_block_kernel(const
 #pragma unroll
       for (int pr = 0; pr < NPROJ; ++pr) {
         if constexpr (BITS == 4)
-          S.c[t][pr] = load8(rw[pr], oob_unless(ok, c_off[t] + co));
+          S.c[t][pr] = load8_nt(rw[pr], oob_unless(ok, c_off[t] + co));
         else
-          S.c[t][pr] = load16(rw[pr], oob_unless(ok, c_off[t] + co));
+          S.c[t][pr] = load16_nt(rw[pr], oob_unless(ok, c_off[t] + co));
       }
   };
 

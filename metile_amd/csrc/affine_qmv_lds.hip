@@ -163,7 +163,7 @@ __device__ __forceinline__ void lds_task(const QmvParams& p, const int group, co
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-      for (int v = 0; v < BITS / 4; ++v) S[pr][v] = load16(rw[pr], ok ? woff + 16u * v : kOOB);
+      for (int v = 0; v < BITS / 4; ++v) S[pr][v] = load16_nt(rw[pr], ok ? woff + 16u * v : kOOB);
   };
   // The first EARLY stages are requested before the scales and activations are parked, the
   // rest after: requests behind the bulk of the grid's code stream would otherwise hold up
