@@ -123,8 +123,8 @@ __global__ __launch_bounds__(64 * kGemvMaxWaves) void affine_gemv_kernel(const Q
         S.q[pr][j] = load16_nt(rw[pr], oob_unless(ok, col * p.col_stride + wo));
         const uint32_t go =
             oob_unless(ok, (col * (uint32_t)groups_per_row + (uint32_t)(k0 >> gshift)) * 2u);
-        S.s[pr][j] = load2(rs[pr], go);
-        S.b[pr][j] = load2(rb[pr], go);
+        S.s[pr][j] = load2_nt(rs[pr], go);
+        S.b[pr][j] = load2_nt(rb[pr], go);
       }
 #pragma unroll
     for (int m = 0; m < ROWS; ++m)

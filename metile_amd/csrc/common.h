@@ -46,14 +46,18 @@ constexpr int kCachePolicyNt = 2;  // the buffer instructions' nt bit on gfx950
 __device__ __forceinline__ u32x4 load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
-// Streaming forms (non-temporal hint, `nt`) for data each launch reads once: the packed codes
-// of the small-row kernels (measured, one-row GEMV over weights 2.5x the MALL: SwiGLU 5.54 ->
-// 5.19 us, down 4.35 -> 4.14 us).
+// Streaming forms (non-temporal hint, `nt`) for data each launch reads once: the small-row
+// kernels' packed codes (measured, one-row GEMV over weights 2.5x the MALL: SwiGLU 5.54 -> 5.19
+// us, down 4.35 -> 4.14 us), the GEMV's scales and biases (down 4.17 -> 4.10 us; the staged
+// kernel's scale staging measured slower with it) and dense weights of one-chunk launches.
 __device__ __forceinline__ u32x4 load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCachePolicyNt);
 }
 __device__ __forceinline__ u32x2 load8_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCachePolicyNt);
+}
+__device__ __forceinline__ uint16_t load2_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kCachePolicyNt);
 }
 __device__ __forceinline__ u32x2 load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);

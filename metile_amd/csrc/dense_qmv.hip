@@ -74,7 +74,10 @@ constexpr int dense_lds_units() {
   return loop > red ? loop : red;
 }
 
-template <int DT, int MT, int NPROJ, int STAGES, bool XLDS>
+// NT: weights read with the non-temporal hint. One row chunk reads each weight line once (M=1
+// MLP 25.0 -> 22.5 us, M=64 36.5 -> 34.4 us); with two chunks the second reads the lines the
+// first left in L2 (M=128 48.6 -> 54.0 us with the hint), so those launches go without it.
+template <int DT, int MT, int NPROJ, int STAGES, bool XLDS, bool NT>
 __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_kernel(
     const DenseParams args) {
   const DenseParams p = preload_args(args);  // all arguments in one batch of scalar loads
@@ -146,7 +149,10 @@ __global__ __launch_bounds__(kThreads, dense_occupancy<MT>()) void dense_qmv_ker
 #pragma unroll
     for (int pr = 0; pr < NPROJ; ++pr)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) S.w[pr][e] = load16(rw[pr], oob_unless(ok, woff + e * w_step8));
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t off = oob_unless(ok, woff + e * w_step8);
+        S.w[pr][e] = NT ? load16_nt(rw[pr], off) : load16(rw[pr], off);
+      }
 #pragma unroll
     for (int rt = 0; rt < MT; ++rt) {
       const uint32_t xoff = x_row[rt] + (uint32_t)st * 128u;
@@ -316,26 +322,33 @@ constexpr int dense_stages() {
   return s < 1 ? 1 : (s > 4 ? 4 : s);
 }
 
-template <int DT, int NPROJ>
-hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
-  // Rows per chunk (grid z): the instance is chosen by the rows of one chunk.
-  const int rows = p.row_chunk ? p.row_chunk : p.M;
-  const dim3 grid(p.N / 32, p.ksplit, p.row_chunk ? (p.M + p.row_chunk - 1) / p.row_chunk : 1);
+template <int DT, int NPROJ, bool NT>
+hipError_t launch_dense_rows(const DenseParams& p, int rows, dim3 grid, hipStream_t stream) {
   // Activations staged through LDS above 8 rows (at fewer rows most operand lanes read zero
   // and the direct loads touch few lines).
   if (rows <= 8) {
-    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), false>
+    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), false, NT>
         <<<grid, kThreads, 0, stream>>>(p);
   } else if (rows <= 32) {
-    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), true>
+    dense_qmv_kernel<DT, 1, NPROJ, dense_stages<NPROJ, 1>(), true, NT>
         <<<grid, kThreads, 0, stream>>>(p);
   } else if (rows <= 64) {
-    dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>(), true>
+    dense_qmv_kernel<DT, 2, NPROJ, dense_stages<NPROJ, 2>(), true, NT>
         <<<grid, kThreads, 0, stream>>>(p);
   } else {
     return hipErrorInvalidValue;  // more than 64 rows run as row chunks (row_chunk)
   }
   return hipGetLastError();
+}
+
+template <int DT, int NPROJ>
+hipError_t launch_dense_dt(const DenseParams& p, hipStream_t stream) {
+  // Rows per chunk (grid z): the instance is chosen by the rows of one chunk.
+  const int rows = p.row_chunk ? p.row_chunk : p.M;
+  const int chunks = p.row_chunk ? (p.M + p.row_chunk - 1) / p.row_chunk : 1;
+  const dim3 grid(p.N / 32, p.ksplit, chunks);
+  return chunks == 1 ? launch_dense_rows<DT, NPROJ, true>(p, rows, grid, stream)
+                     : launch_dense_rows<DT, NPROJ, false>(p, rows, grid, stream);
 }
 
 }  // namespace
