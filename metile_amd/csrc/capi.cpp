@@ -492,8 +492,8 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
       const mt_qmv_plan g{MT_QMV_GEMV4, 1, N / (4 * cg), w, 0};
       if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, g).empty()) out.push_back(g);
     }
-  // Column blocks: one or two workgroups per CU, or blocks of 16 or 32 columns; 4 or 8 waves;
-  // K unsplit or in 4 splits.
+  // Column blocks: one or two workgroups per CU, or blocks of 16 or 32 columns; 4, 6 or 8 waves
+  // (six: config 3 at 16 rows 25.6 -> 25.2 us); K unsplit or in 4 splits.
   {
     const int kCus = device_cus();
     std::vector<int> strips;
@@ -503,7 +503,7 @@ std::vector<mt_qmv_plan> qmv_candidates(int rows, int K, int N, int nproj, int g
       const Plan p = split_plan(steps, ks);
       if (p.ksplit != ks) continue;
       for (int s : strips)
-        for (int w : {8, 4}) {
+        for (int w : {8, 6, 4}) {
           const mt_qmv_plan b{MT_QMV_BLOCK, ks, s, w, 0};
           if (qmv_plan_problem(rows, K, N, nproj, group_size, bits, b).empty()) out.push_back(b);
         }

@@ -225,7 +225,7 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
                if fits(c, w) and n % (c * groups(w)) == 0)
         if bucket <= 4 else [])
     # column blocks: one or two workgroups per CU (256 CUs on the host, with no device), or
-    # blocks of 16 or 32 columns, at most 64 wide in either code layout; 4 or 8 waves; K unsplit
+    # blocks of 16 or 32 columns, at most 64 wide in either code layout; 4, 6 or 8 waves; K unsplit
     # or in 4 equal splits; groups of 64 or more
     align = 16 // bits
     # the 4x4x4-MFMA GEMV: up to 4 rows of 4-bit codes, 1, 2 or 4 groups of 4 columns per
@@ -247,7 +247,7 @@ def test_candidates_are_valid_and_include_the_planner(shape, clean_plans):
             assert c.ksplit == 1 and c.workgroups == c.strips
         elif c.kernel == "block":
             assert g >= 64 and rows <= 32 and c.order == 0
-            assert c.ksplit in (1, 4) and c.tiles in (4, 8)
+            assert c.ksplit in (1, 4) and c.tiles in (4, 6, 8)
             assert c.strips in (256, 512, n // 16, n // 32)
             assert max(-(-n // c.strips), -(-(n // align) // c.strips) * align) <= 64
         else:
